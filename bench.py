@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""bench.py — INT8-KV split-KV decode attention on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload decode]
+
+Default workload is the BASELINE headline: decode attention over a contiguous
+INT8 KV cache, B=32 H=32 D=128 ctx=8192 (2 GiB of K+V), 1% of channels x8
+before per-token quantization.  One step = one decode call over the whole
+batch (split kernel + combine kernel), inputs already resident in HBM.
+
+Prints ONE JSON line (rank 0).  `value` is the effective KV-read bandwidth
+(2*B*H*S*D bytes / step time) in TB/s; `roofline` prices the same bytes
+against the 8 TB/s HBM peak; `cpu_baseline` is the CPU oracle (C, OpenMP)
+timed on a bounded sample of the same heads on this host.
+Everything else (per-config details) goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO_DIR = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(REPO_DIR, "int8-transformer-kernels_amd")
+sys.path.insert(0, REPO_DIR)
+sys.path.insert(0, PKG_DIR)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = ("decode attn µs + effective KV-read TB/s (% HBM peak), "
+          "B=32 H=32 D=128 8K ctx")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def cpu_baseline_decode(case, B, H, D, S, budget_s=12.0):
+    """Time the C oracle (all host cores) on a growing sample of (b,h) heads."""
+    import numpy as np
+    from oracle import oracle_c
+
+    BH = B * H
+    Q = case["Qi"].reshape(BH, D)
+    K = case["Ki"].reshape(BH, S, D)
+    V = case["Vi"].reshape(BH, S, D)
+    sQ = case["sQ"].reshape(BH)
+    sK = case["sK"].reshape(BH, S)
+    sV = case["sV"].reshape(BH, S)
+    threads = oracle_c.max_threads()
+    n, spent, done_bytes, heads = 4, 0.0, 0, 0
+    while spent < budget_s and heads < BH:
+        n = min(n, BH - heads)
+        sl = slice(heads, heads + n)
+        args = [t[sl].cpu().numpy() for t in (Q, K, V, sQ, sK, sV)]
+        t0 = time.perf_counter()
+        oracle_c.decode_attention(*args, threads=threads)
+        spent += time.perf_counter() - t0
+        done_bytes += 2 * n * S * D
+        heads += n
+        n *= 2
+    tbs = done_bytes / spent / 1e12
+    return dict(value=tbs, unit="TB/s", cores=threads, kind="port",
+                sample=f"C oracle (float64, OpenMP) on {heads} of {BH} (b,h) heads of the "
+                       f"same B{B} H{H} D{D} S{S} inputs; {spent:.1f} s of CPU time; "
+                       f"host os.cpu_count()={os.cpu_count()}",
+                seconds=spent, heads=heads)
+
+
+def bench_decode(args):
+    import torch
+
+    import int8k_capi as capi
+    import workloads
+
+    B, H, D, S = args.batch, args.heads, args.head_dim, args.ctx
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] generating decode inputs B{B} H{H} D{D} S{S} (outliers 1% x8)")
+    case = workloads.decode_case(B, H, D, S, seed=args.seed, outlier_frac=0.01, device=dev)
+    BH = B * H
+    Q = case["Qi"].reshape(BH, D)
+    K = case["Ki"].reshape(BH, S, D)
+    V = case["Vi"].reshape(BH, S, D)
+    sQ, sK, sV = case["sQ"].reshape(-1), case["sK"].reshape(-1), case["sV"].reshape(-1)
+    out = torch.empty((BH, D), dtype=torch.float16, device=dev)
+    ws = torch.empty(max(capi.decode_workspace_bytes(BH, S, D, args.nsplit), 1),
+                     dtype=torch.uint8, device=dev)
+    nsplit = capi.decode_num_splits(BH, S, D, args.nsplit)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        capi.decode_attention(Q, K, V, sQ, sK, sV, nsplit=args.nsplit, out=out, workspace=ws)
+
+    ms = time_steps(step, args.steps, args.warmup, stream)
+    kv_bytes = 2 * BH * S * D
+    scale_bytes = 2 * BH * S * 4
+    tbs = kv_bytes / (ms * 1e-3) / 1e12
+    achieved_gbs = kv_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] nsplit={nsplit} units={BH * nsplit} step={ms * 1e3:.1f} us "
+        f"KV-read {tbs:.3f} TB/s ({achieved_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s); "
+        f"scale-inclusive {(kv_bytes + scale_bytes) / (ms * 1e-3) / 1e12:.3f} TB/s")
+
+    # sanity: a few heads against the oracle (cheap, untimed)
+    import numpy as np
+    from oracle import oracle_c
+    rows = np.arange(0, BH, max(1, BH // 8))
+    ref = oracle_c.decode_attention(Q[rows].cpu().numpy(), K[rows].cpu().numpy(),
+                                    V[rows].cpu().numpy(), sQ.reshape(BH)[rows].cpu().numpy(),
+                                    sK.reshape(BH, S)[rows].cpu().numpy(),
+                                    sV.reshape(BH, S)[rows].cpu().numpy())
+    err = float(np.abs(out[rows].float().cpu().numpy() - ref).max())
+    log(f"[bench] parity sample ({len(rows)} heads): max_abs={err:.2e}")
+    if not (err <= 2e-2):
+        raise SystemExit(f"decode output does not match the oracle (max_abs={err})")
+
+    res = {
+        "metric": METRIC,
+        "value": round(tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(achieved_gbs / HBM_PEAK_GBS * 100, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1), 1% channels x8, per-token int8)",
+        "config": {"workload": f"int8-kv decode attention B={B} H={H} D={D} ctx={S}",
+                   "batch": B, "heads": H, "head_dim": D, "ctx": S, "nsplit": nsplit,
+                   "kv_bytes": kv_bytes, "scale_bytes": scale_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "decode_split_kernel + decode_combine_kernel (one step)"},
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline_decode(case, B, H, D, S, budget_s=args.cpu_budget)
+        log(f"[bench] cpu baseline: {cb['value'] * 1e3:.3f} GB/s on {cb['cores']} threads "
+            f"({cb['heads']} heads, {cb['seconds']:.1f} s)")
+        res["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    else:
+        res["cpu_baseline"] = None
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--heads", type=int, default=32)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--nsplit", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=20241201)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(decode shards over (b,h) with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    res = bench_decode(args)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,84 @@
+/*
+ * int8k.h — C ABI of the MI355X (gfx950) INT8 transformer-inference kernels.
+ *
+ * Every entry point takes plain device pointers, element counts and an opaque
+ * HIP stream (a hipStream_t passed as void*; NULL means the legacy default
+ * stream).  Nothing here allocates device memory: operations that need
+ * scratch take a caller-owned workspace whose size comes from the matching
+ * *_workspace_bytes() query.  Every call returns an int8k_status; launches are
+ * asynchronous on the given stream and are checked with hipGetLastError().
+ *
+ * Numerical contract (shared with the reference L1 launchers cited below):
+ *   - per-token symmetric scales: x ~= q * s, s = max(|row|, 1e-8) / 127,
+ *     q = round-half-even(x / s) clamped to [-128, 127];
+ *   - fp16 means IEEE binary16 stored in uint16_t;
+ *   - attention scale 1/sqrt(head_dim), softmax in fp32, output fp16.
+ *
+ * The entry points replace the raw-pointer C++ launchers that the reference's
+ * torch binding forward-declares at kernels/int8_ext.cu:26-70.
+ */
+#ifndef INT8K_H
+#define INT8K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INT8K_ABI_VERSION 1
+
+typedef enum int8k_status {
+    INT8K_OK = 0,
+    INT8K_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative or zero size, shape mismatch */
+    INT8K_ERR_UNSUPPORTED = 2,      /* valid but unsupported configuration (e.g. head_dim) */
+    INT8K_ERR_WORKSPACE = 3,        /* workspace missing or smaller than the query says */
+    INT8K_ERR_MISALIGNED = 4,       /* a pointer violates the documented alignment */
+    INT8K_ERR_HIP = 5               /* the HIP runtime reported an error at launch */
+} int8k_status;
+
+/* Human-readable text for a status code (static storage, never NULL). */
+const char* int8k_status_string(int status);
+
+/* INT8K_ABI_VERSION of the built library. */
+int int8k_abi_version(void);
+
+/* Text of the last HIP error seen by this thread's most recent failing call
+ * ("" if none). */
+const char* int8k_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Split-KV decode attention (seq_q == 1) over a contiguous INT8 KV cache.   */
+/*                                                                          */
+/* Replaces int8_decode_attention_forward(Q, K, V, out, scale_Q, scale_K,   */
+/* scale_V, BH, S, head_dim) — kernels/int8_decode_attention.cu:443-447,     */
+/* declared at kernels/int8_ext.cu:33-37.                                    */
+/*                                                                          */
+/*   Q   int8 [BH, D]        sQ float [BH]                                   */
+/*   K,V int8 [BH, S, D]     sK, sV float [BH*S]  (index bh*S + j)           */
+/*   out fp16 [BH, D]                                                        */
+/*   out[bh] = sum_j softmax_j(q.k_j * sQ*sK_j / sqrt(D)) * (v_j * sV_j)     */
+/*                                                                          */
+/* D must be 64 or 128 (as the reference binding checks, kernels/int8_ext.cu */
+/* :160-161); S >= 1.  Q, K, V must be 16-byte aligned.  nsplit = 0 picks    */
+/* the split count automatically (sized for 256 CUs); a positive value       */
+/* forces that many KV chunks per (b,h) (clamped to what S allows) — the     */
+/* result is independent of it up to fp32 rounding.                          */
+/* ------------------------------------------------------------------------ */
+size_t int8k_decode_attention_workspace_bytes(int BH, int S, int head_dim, int nsplit);
+
+int int8k_decode_attention_forward(
+    const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int BH, int S, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* The split count the forward call uses for this shape (after clamping). */
+int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INT8K_H */

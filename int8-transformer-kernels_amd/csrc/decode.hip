@@ -1,0 +1,381 @@
+// decode.hip — split-KV flash-decoding over a contiguous INT8 KV cache (gfx950).
+//
+// Computes, for every (b,h) = bh and a single query token,
+//     out[bh,:] = sum_j softmax_j(score_j) * (V[bh,j,:] * sV[bh*S+j])
+//     score_j   = (Q[bh,:] . K[bh,j,:]) * sQ[bh] * sK[bh*S+j] / sqrt(D)
+// which is the contract of the reference launcher
+// int8_decode_attention_forward (kernels/int8_decode_attention.cu:443-547) and
+// of its partial/combine pair (kernels/int8_decode_attention.cu:274-426).
+//
+// Design (CDNA4 first, not a translation of the warp-per-unit CUDA kernel):
+//
+//  * HBM-bound: one pass over K and V (2*BH*S*D bytes) dominates.  Each wave64
+//    lane issues 16-byte global loads; a wave's load instruction covers
+//    64 x 16 B = 1 KiB made of whole 128-byte (D=128) or 64-byte (D=64) rows.
+//  * Lane layout: LPR = D/16 lanes share a row (lane s of the group holds row
+//    bytes [16s, 16s+16)); G = 64/LPR row-groups per wave.  One wave
+//    iteration covers R = G*NSLOT rows: group g owns rows g*NSLOT .. +NSLOT-1
+//    of the block, one per load slot, so every slot of every lane is an
+//    immediate offset from one base address.
+//  * QK: 4 v_dot4_i32_i8 per slot per lane (exact int32), then a DPP sum over
+//    the LPR lanes of the group (no LDS).  The group's lanes all hold the score.
+//  * Softmax: every row-group keeps its own online-softmax state (m, l) in the
+//    log2 domain and its own fp32 accumulator for the 16 dims its lane holds,
+//    so the hot loop has no cross-group traffic at all.  The G group states of
+//    a wave are merged once, at the end of the wave's KV chunk.
+//  * PV: each V byte is converted with one SDWA v_cvt_f32_i32 and folded in
+//    with one FMA: acc += (p_j * sV_j) * v_j.
+//  * Split-KV: a work unit = one wave = one (bh, chunk).  The split count is
+//    chosen on the host so that BH*nsplit waves fill 256 CUs several times
+//    over; partial states (m, l, acc[D]) go to the workspace and a combine
+//    kernel merges them with the log-sum-exp rule into fp16.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+
+#include "int8k_common.h"
+
+namespace int8k {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlockThreads = 64 * kWavesPerBlock;
+constexpr int kSlots = 8;  // rows per row-group per wave iteration
+
+template <int D>
+struct DecodeGeom {
+    static_assert(D == 64 || D == 128, "decode supports head_dim 64 and 128");
+    static constexpr int kLanesPerRow = D / 16;
+    static constexpr int kGroups = 64 / kLanesPerRow;
+    static constexpr int kRowsPerIter = kGroups * kSlots;
+};
+
+// Rows per wave iteration for a head dim (host side).
+inline int rows_per_iter(int D) { return (64 / (D / 16)) * kSlots; }
+
+struct SplitPlan {
+    int nsplit;
+    int chunk;
+};
+
+inline int env_target_units() {
+    static const int v = [] {
+        const char* e = std::getenv("INT8K_DECODE_TARGET_UNITS");
+        const int x = e ? std::atoi(e) : 0;
+        return x > 0 ? x : 0;
+    }();
+    return v;
+}
+
+// Split-count choice.  A unit is one wave; 256 CUs hold 2048 waves at the
+// kernel's occupancy (8 waves/CU), so aim for ~4 units per wave slot to keep
+// the tail short while each chunk still spans several loop iterations.
+SplitPlan plan_splits(int BH, int S, int D, int nsplit_req) {
+    const int R = rows_per_iter(D);
+    const long long max_split = ceil_div(S, R);
+    long long ns;
+    if (nsplit_req > 0) {
+        ns = nsplit_req;
+    } else {
+        const int target = env_target_units() > 0 ? env_target_units() : 8192;
+        ns = ceil_div(target, BH);
+        // keep at least 4 iterations per unit unless S is short
+        const long long by_len = std::max<long long>(1, ceil_div(S, 4LL * R));
+        ns = std::min(ns, by_len);
+    }
+    ns = std::max<long long>(1, std::min(ns, max_split));
+    long long chunk = round_up((size_t)ceil_div(S, ns), (size_t)R);
+    ns = ceil_div(S, chunk);
+    return SplitPlan{(int)ns, (int)chunk};
+}
+
+struct Int4 {
+    int x, y, z, w;
+};
+
+__device__ __forceinline__ Int4 load16(const int8_t* p) {
+    const int4 v = *reinterpret_cast<const int4*>(p);
+    return Int4{v.x, v.y, v.z, v.w};
+}
+
+__device__ __forceinline__ void fma_bytes(float* acc, int word, float w) {
+    acc[0] = fmaf(w, sbyte_to_f32<0>(word), acc[0]);
+    acc[1] = fmaf(w, sbyte_to_f32<1>(word), acc[1]);
+    acc[2] = fmaf(w, sbyte_to_f32<2>(word), acc[2]);
+    acc[3] = fmaf(w, sbyte_to_f32<3>(word), acc[3]);
+}
+
+template <int D>
+__device__ __forceinline__ int group_sum(int v) {
+    if constexpr (DecodeGeom<D>::kLanesPerRow == 8) return group8_sum(v);
+    else return group4_sum(v);
+}
+
+// One wave iteration over NSLOT rows per group.  MASKED handles the last
+// partial block of a chunk: rows >= j1 get score -inf and weight 0 (their
+// loads are redirected to row j1-1, which is in bounds).
+template <int D, bool MASKED, bool VEC_SCALES>
+__device__ __forceinline__ void decode_iter(
+    const int8_t* __restrict__ Kbh, const int8_t* __restrict__ Vbh,
+    const float* __restrict__ sKbh, const float* __restrict__ sVbh,
+    int row0, int j1, int sub, const Int4& q, float qscale,
+    float& m, float& l, float* acc) {
+    constexpr int NS = kSlots;
+    Int4 kv[NS], vv[NS];
+    float sk[NS], sv[NS];
+
+    if constexpr (!MASKED) {
+        const int8_t* kp = Kbh + (size_t)row0 * D + sub * 16;
+        const int8_t* vp = Vbh + (size_t)row0 * D + sub * 16;
+#pragma unroll
+        for (int t = 0; t < NS; ++t) kv[t] = load16(kp + t * D);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) vv[t] = load16(vp + t * D);
+        if constexpr (VEC_SCALES) {
+#pragma unroll
+            for (int t = 0; t < NS; t += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(sKbh + row0 + t);
+                const float4 b = *reinterpret_cast<const float4*>(sVbh + row0 + t);
+                sk[t] = a.x; sk[t + 1] = a.y; sk[t + 2] = a.z; sk[t + 3] = a.w;
+                sv[t] = b.x; sv[t + 1] = b.y; sv[t + 2] = b.z; sv[t + 3] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NS; ++t) { sk[t] = sKbh[row0 + t]; sv[t] = sVbh[row0 + t]; }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const int r = min(row0 + t, j1 - 1);
+            kv[t] = load16(Kbh + (size_t)r * D + sub * 16);
+            vv[t] = load16(Vbh + (size_t)r * D + sub * 16);
+            sk[t] = sKbh[r];
+            sv[t] = sVbh[r];
+        }
+    }
+
+    // QK^T: exact int32 dot per row, summed over the LPR lanes of the group.
+    float sc[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        int d = __builtin_amdgcn_sdot4(q.x, kv[t].x, 0, false);
+        d = __builtin_amdgcn_sdot4(q.y, kv[t].y, d, false);
+        d = __builtin_amdgcn_sdot4(q.z, kv[t].z, d, false);
+        d = __builtin_amdgcn_sdot4(q.w, kv[t].w, d, false);
+        d = group_sum<D>(d);
+        sc[t] = static_cast<float>(d) * qscale * sk[t];
+        if constexpr (MASKED) {
+            if (row0 + t >= j1) sc[t] = -INFINITY;
+        }
+    }
+
+    // Online softmax (log2 domain) for this group's NSLOT rows.
+    float mx = sc[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) mx = fmaxf(mx, sc[t]);
+    const float m_new = fmaxf(m, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float corr = fast_exp2(m - m_use);
+    l *= corr;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        const float p = fast_exp2(sc[t] - m_use);
+        l += p;
+        float w = p * sv[t];
+        if constexpr (MASKED) {
+            if (row0 + t >= j1) w = 0.f;
+        }
+        fma_bytes(acc + 0, vv[t].x, w);
+        fma_bytes(acc + 4, vv[t].y, w);
+        fma_bytes(acc + 8, vv[t].z, w);
+        fma_bytes(acc + 12, vv[t].w, w);
+    }
+    m = m_new;
+}
+
+// Pass 1: one wave per (bh, split); writes the unnormalised partial state.
+template <int D, bool VEC_SCALES>
+__global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ K,
+    const int8_t* __restrict__ V, const float* __restrict__ sQ,
+    const float* __restrict__ sK, const float* __restrict__ sV,
+    float* __restrict__ part_ml, float* __restrict__ part_acc,
+    int S, int nsplit, int chunk, int units, float qk_scale_log2) {
+    using G = DecodeGeom<D>;
+    const int lane = threadIdx.x & 63;
+    const int unit = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (unit >= units) return;  // whole wave exits; no block barrier below
+    const int bh = unit / nsplit;
+    const int sp = unit - bh * nsplit;
+    const int j0 = sp * chunk;
+    const int j1 = min(S, j0 + chunk);
+
+    const int sub = lane % G::kLanesPerRow;
+    const int grp = lane / G::kLanesPerRow;
+
+    const Int4 q = load16(Q + (size_t)bh * D + sub * 16);
+    const float qscale = sQ[bh] * qk_scale_log2;
+
+    const int8_t* Kbh = K + (size_t)bh * S * D;
+    const int8_t* Vbh = V + (size_t)bh * S * D;
+    const float* sKbh = sK + (size_t)bh * S;
+    const float* sVbh = sV + (size_t)bh * S;
+
+    float m = -INFINITY, l = 0.f;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+
+    int base = j0;
+    for (; base + G::kRowsPerIter <= j1; base += G::kRowsPerIter)
+        decode_iter<D, false, VEC_SCALES>(Kbh, Vbh, sKbh, sVbh, base + grp * kSlots, j1, sub,
+                                          q, qscale, m, l, acc);
+    if (base < j1)
+        decode_iter<D, true, VEC_SCALES>(Kbh, Vbh, sKbh, sVbh, base + grp * kSlots, j1, sub,
+                                         q, qscale, m, l, acc);
+
+    // Merge the G row-group states of this wave (lanes with equal `sub`).
+    float M = m;
+#pragma unroll
+    for (int off = G::kLanesPerRow; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+    const float f = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
+    float L = l * f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= f;
+#pragma unroll
+    for (int off = G::kLanesPerRow; off < 64; off <<= 1) {
+        L += __shfl_xor(L, off);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
+    }
+    if (grp == 0) {
+        float4* dst = reinterpret_cast<float4*>(part_acc + (size_t)unit * D + sub * 16);
+        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+        dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+        if (sub == 0) {
+            part_ml[2 * (size_t)unit] = M;
+            part_ml[2 * (size_t)unit + 1] = L;
+        }
+    }
+}
+
+// Pass 2: one wave per bh merges its nsplit partial states into fp16.
+template <int D>
+__global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
+    const float* __restrict__ part_ml, const float* __restrict__ part_acc,
+    uint16_t* __restrict__ out, int BH, int nsplit) {
+    constexpr int DPL = D / 64;  // dims per lane
+    const int lane = threadIdx.x & 63;
+    const int bh = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (bh >= BH) return;
+    const float* ml = part_ml + 2 * (size_t)bh * nsplit;
+
+    float M = -INFINITY;
+    for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+    const float M_use = (M == -INFINITY) ? 0.f : M;
+
+    float L = 0.f;
+    for (int s = lane; s < nsplit; s += 64) L += ml[2 * s + 1] * fast_exp2(ml[2 * s] - M_use);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) L += __shfl_xor(L, off);
+
+    float acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+    const float* pa = part_acc + (size_t)bh * nsplit * D + lane * DPL;
+    for (int s = 0; s < nsplit; ++s) {
+        const float w = fast_exp2(ml[2 * s] - M_use);
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] = fmaf(pa[(size_t)s * D + i], w, acc[i]);
+    }
+    const float inv = 1.f / L;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i)
+        out[(size_t)bh * D + lane * DPL + i] = f32_to_f16_bits(acc[i] * inv);
+}
+
+struct DecodeWorkspace {
+    float* part_ml;
+    float* part_acc;
+    size_t bytes;
+};
+
+DecodeWorkspace carve(void* ws, long long units, int D) {
+    const size_t ml_bytes = round_up((size_t)units * 2 * sizeof(float), kWorkspaceAlign);
+    const size_t acc_bytes = round_up((size_t)units * D * sizeof(float), kWorkspaceAlign);
+    char* p = static_cast<char*>(ws);
+    return DecodeWorkspace{reinterpret_cast<float*>(p), reinterpret_cast<float*>(p + ml_bytes),
+                           ml_bytes + acc_bytes};
+}
+
+template <int D>
+int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+                  const float* sQ, const float* sK, const float* sV, int BH, int S,
+                  const SplitPlan& plan, const DecodeWorkspace& w, hipStream_t stream) {
+    const long long units = (long long)BH * plan.nsplit;
+    const float qk_scale_log2 = (1.0f / std::sqrt((float)D)) * kLog2e;
+    const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
+    const bool vec_scales = (S % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
+    if (vec_scales)
+        decode_split_kernel<D, true><<<grid, kBlockThreads, 0, stream>>>(
+            Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, S, plan.nsplit, plan.chunk, (int)units,
+            qk_scale_log2);
+    else
+        decode_split_kernel<D, false><<<grid, kBlockThreads, 0, stream>>>(
+            Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, S, plan.nsplit, plan.chunk, (int)units,
+            qk_scale_log2);
+    int st = check_launch("decode_split_kernel");
+    if (st != INT8K_OK) return st;
+    const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));
+    decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out, BH,
+                                                                  plan.nsplit);
+    return check_launch("decode_combine_kernel");
+}
+
+}  // namespace
+}  // namespace int8k
+
+using namespace int8k;
+
+extern "C" int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit) {
+    if (BH <= 0 || S <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
+    return plan_splits(BH, S, head_dim, nsplit).nsplit;
+}
+
+extern "C" size_t int8k_decode_attention_workspace_bytes(int BH, int S, int head_dim, int nsplit) {
+    if (BH <= 0 || S <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
+    const SplitPlan plan = plan_splits(BH, S, head_dim, nsplit);
+    return carve(nullptr, (long long)BH * plan.nsplit, head_dim).bytes;
+}
+
+extern "C" int int8k_decode_attention_forward(
+    const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int BH, int S, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    clear_last_error();
+    if (!Q || !K || !V || !out || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
+    if (BH <= 0 || S <= 0 || nsplit < 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (head_dim != 64 && head_dim != 128) return INT8K_ERR_UNSUPPORTED;
+    if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) ||
+        !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4) ||
+        !aligned_to(out, 2))
+        return INT8K_ERR_MISALIGNED;
+    const SplitPlan plan = plan_splits(BH, S, head_dim, nsplit);
+    const long long units = (long long)BH * plan.nsplit;
+    if (units >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    const DecodeWorkspace w = carve(workspace, units, head_dim);
+    if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
+    if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;
+    if (head_dim == 128)
+        return launch_decode<128>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, plan, w,
+                                  as_stream(stream));
+    return launch_decode<64>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, plan, w,
+                             as_stream(stream));
+}

@@ -1,0 +1,90 @@
+// int8k_common.h — shared host/device helpers for the gfx950 INT8 kernels.
+//
+// Internal header: only the .hip translation units of libint8k include it.
+// Everything here is written for CDNA4 (wave64, DPP, v_dot4, MFMA); there is
+// no other target.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "int8k.h"
+
+namespace int8k {
+
+// ---------------------------------------------------------------- host side
+
+// Records the text of a failing HIP call for int8k_last_error().
+void set_last_error(const char* what, hipError_t err);
+void clear_last_error();
+
+// Checks the launch that was just enqueued on this thread.
+inline int check_launch(const char* what) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        set_last_error(what, err);
+        return INT8K_ERR_HIP;
+    }
+    return INT8K_OK;
+}
+
+inline bool aligned_to(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+// Workspace sub-allocations are carved at this granularity.
+constexpr size_t kWorkspaceAlign = 256;
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// -------------------------------------------------------------- device side
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x on the transcendental unit (v_exp_f32).  exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane moves inside a row of 16 lanes (DPP, no LDS traffic).
+// quad_perm [1,0,3,2]: lane ^ 1
+__device__ __forceinline__ int dpp_xor1(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+}
+// quad_perm [2,3,0,1]: lane ^ 2
+__device__ __forceinline__ int dpp_xor2(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+}
+// row_half_mirror: lane i of each 8-lane half-row reads lane 7-i.
+__device__ __forceinline__ int dpp_half_mirror(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+}
+
+// Sum over each aligned group of 4 lanes; every lane of the group gets it.
+__device__ __forceinline__ int group4_sum(int v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    return v;
+}
+// Sum over each aligned group of 8 lanes; every lane of the group gets it.
+__device__ __forceinline__ int group8_sum(int v) {
+    v = group4_sum(v);
+    v += dpp_half_mirror(v);
+    return v;
+}
+
+// Signed byte i (0..3) of a packed dword as fp32 (one SDWA v_cvt_f32_i32).
+template <int I>
+__device__ __forceinline__ float sbyte_to_f32(int w) {
+    return static_cast<float>(static_cast<int8_t>((w >> (8 * I)) & 0xff));
+}
+
+// fp32 -> fp16 bits, round to nearest even.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+    return __half_as_ushort(__float2half_rn(x));
+}
+
+}  // namespace int8k

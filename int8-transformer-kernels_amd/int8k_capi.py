@@ -1,0 +1,121 @@
+"""ctypes binding of libint8k's C ABI (include/int8k.h).
+
+This is the binding a Python caller that does not want the torch extension
+would use; the tests drive the kernels through it so parity is checked at the
+C boundary itself.  torch tensors are used only to hold device memory and to
+name the current HIP stream.  Loading fails loudly if the library was not
+built — there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(PKG_DIR, "libint8k.so")
+HEADER_PATH = os.path.join(REPO_DIR, "include", "int8k.h")
+
+INT8K_OK = 0
+INT8K_ERR_INVALID_ARGUMENT = 1
+INT8K_ERR_UNSUPPORTED = 2
+INT8K_ERR_WORKSPACE = 3
+INT8K_ERR_MISALIGNED = 4
+INT8K_ERR_HIP = 5
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+_LL = ctypes.c_longlong
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "int8k_status_string": (ctypes.c_char_p, [_I]),
+    "int8k_abi_version": (_I, []),
+    "int8k_last_error": (ctypes.c_char_p, []),
+    "int8k_decode_attention_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "int8k_decode_attention_num_splits": (_I, [_I, _I, _I, _I]),
+    "int8k_decode_attention_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
+}
+
+_lib = None
+
+
+class Int8kError(RuntimeError):
+    def __init__(self, op: str, status: int):
+        lib = load()
+        msg = lib.int8k_status_string(status).decode()
+        detail = lib.int8k_last_error().decode()
+        super().__init__(f"{op}: {msg}" + (f" — {detail}" if detail else ""))
+        self.status = status
+
+
+def declared_symbols() -> list[str]:
+    """Every function name declared in include/int8k.h."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(int8k_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with "
+                f"`python {os.path.join(PKG_DIR, 'build.py')}` (no CPU fallback exists)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(t):
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def check(op: str, status: int) -> None:
+    if status != INT8K_OK:
+        raise Int8kError(op, status)
+
+
+# --------------------------------------------------------------------------
+# decode
+# --------------------------------------------------------------------------
+
+
+def decode_workspace_bytes(BH: int, S: int, D: int, nsplit: int = 0) -> int:
+    return load().int8k_decode_attention_workspace_bytes(BH, S, D, nsplit)
+
+
+def decode_num_splits(BH: int, S: int, D: int, nsplit: int = 0) -> int:
+    return load().int8k_decode_attention_num_splits(BH, S, D, nsplit)
+
+
+def decode_attention(Qi, Ki, Vi, sQ, sK, sV, nsplit: int = 0, out=None, workspace=None):
+    """Qi [BH,D] int8, Ki/Vi [BH,S,D] int8, sQ [BH], sK/sV [BH*S] fp32 (device)."""
+    import torch
+
+    BH, D = Qi.shape[0], Qi.shape[-1]
+    S = Ki.numel() // (BH * D)
+    if out is None:
+        out = torch.empty((BH, D), dtype=torch.float16, device=Qi.device)
+    ws_bytes = decode_workspace_bytes(BH, S, D, nsplit)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=Qi.device)
+    st = load().int8k_decode_attention_forward(
+        _ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(out), _ptr(sQ), _ptr(sK), _ptr(sV),
+        BH, S, D, nsplit, _ptr(workspace), workspace.numel(), _stream(Qi))
+    check("int8k_decode_attention_forward", st)
+    return out

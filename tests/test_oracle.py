@@ -1,0 +1,290 @@
+"""Pins the CPU oracle (CPU-only tests).
+
+Each check is chosen so a plausible slip in the oracle (wrong scale index,
+dropped 1/sqrt(D), transposed operand, truncation instead of round-half-even,
+clamp asymmetry, a missing GELU term) fails at least one of them: brute-force
+loops on tiny inputs, closed forms and known-answer datasets of the reference
+(validation/generate_test_data.py: zeros, constant, boundary), invariants, and
+independent library routines (torch SDPA, torch GELU).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import int8_oracle as O
+from oracle import oracle_c as C
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- quantizers
+
+def test_quantize_per_token_kats():
+    x = np.array([[0.0, 0.0, 0.0, 0.0],          # zeros -> scale 1e-8/127, codes 0
+                  [2.0, 2.0, 2.0, 2.0],          # constant -> single code 127
+                  [-4.0, 4.0, 1.0, -1.0],
+                  [1.0, -0.5, 0.25, 127 * 0.5 / 127]], np.float32)
+    q, s = O.quantize_per_token(x)
+    assert q.dtype == np.int8 and s.dtype == np.float32
+    np.testing.assert_array_equal(q[0], 0)
+    assert s[0] == np.float32(np.float32(1e-8) / np.float32(127))
+    np.testing.assert_array_equal(q[1], 127)
+    assert s[1] == np.float32(2.0 / 127)
+    np.testing.assert_array_equal(q[2], [-127, 127, 32, -32])   # 31.75 -> 32
+    assert q[3, 0] == 127 and q[3, 1] == -64  # -63.5 -> -64 (half to even)
+
+
+def test_quantize_round_half_even_and_clamp():
+    # scale 1 exactly: amax 127 -> codes equal rint(x) with ties to even.
+    x = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.49]], np.float32)
+    q, s = O.quantize_per_token(x)
+    assert s[0] == 1.0
+    np.testing.assert_array_equal(q[0], [127, 0, 2, 2, 0, -2, -2, 3])
+
+
+def test_quantize_boundary_dataset_codes():
+    # validation/generate_test_data.py:113-122: |x| in amax*[0.985, 1] lands on +-126/127.
+    g = rng(1)
+    sign = g.integers(0, 2, (64, 128)) * 2 - 1
+    mag = 4.0 * (0.985 + 0.015 * g.random((64, 128)))
+    x = (sign * mag).astype(np.float32)
+    q, s = O.quantize_per_token(x)
+    assert set(np.unique(np.abs(q.astype(np.int32)))) <= {125, 126, 127}
+    assert (np.abs(x - q.astype(np.float32) * s[:, None]) <= s[:, None] / 2 * (1 + 1e-6)).all()
+
+
+def test_quantize_matches_torch_formula():
+    # the reference quantizer written with torch ops (validation/check_decode.py:42-47)
+    x = rng(2).standard_normal((33, 64)).astype(np.float32)
+    t = torch.from_numpy(x)
+    am = t.abs().amax(-1, keepdim=True).clamp(min=1e-8)
+    sc = am / 127.0
+    qt = (t / sc).round().clamp(-128, 127).to(torch.int8)
+    q, s = O.quantize_per_token(x)
+    np.testing.assert_array_equal(q, qt.numpy())
+    np.testing.assert_array_equal(s, sc.squeeze(-1).numpy())
+
+
+def test_quantize_per_channel_w_axis():
+    w = np.zeros((4, 3), np.float32)
+    w[:, 0] = [1, -2, 0.5, 0.0]
+    w[:, 1] = [0.02, 0.01, -0.04, 0.0]
+    q, s = O.quantize_per_channel_w(w)
+    np.testing.assert_allclose(s, [2 / 127, 0.04 / 127, 1e-8 / 127], rtol=1e-7)
+    np.testing.assert_array_equal(q[:, 0], [64, -127, 32, 0])  # 63.5 -> 64 (even)
+    np.testing.assert_array_equal(q[:, 2], 0)
+
+
+# ---------------------------------------------------------------- attention
+
+def brute_decode(Q, K, V, sQ, sK, sV):
+    BH, D = Q.shape
+    S = K.shape[1]
+    out = np.zeros((BH, D))
+    for b in range(BH):
+        sc = []
+        for j in range(S):
+            dot = sum(int(Q[b, d]) * int(K[b, j, d]) for d in range(D))
+            sc.append(dot * float(sQ[b]) * float(sK[b, j]) / math.sqrt(D))
+        m = max(sc)
+        p = [math.exp(x - m) for x in sc]
+        z = sum(p)
+        for d in range(D):
+            out[b, d] = sum(p[j] * float(V[b, j, d]) * float(sV[b, j]) for j in range(S)) / z
+    return out
+
+
+def rand_decode(BH, S, D, seed):
+    g = rng(seed)
+    Q, sQ = O.quantize_per_token(g.standard_normal((BH, D)).astype(np.float32))
+    K, sK = O.quantize_per_token(g.standard_normal((BH, S, D)).astype(np.float32))
+    V, sV = O.quantize_per_token(g.standard_normal((BH, S, D)).astype(np.float32))
+    return Q, K, V, sQ, sK, sV
+
+
+@pytest.mark.parametrize("BH,S,D", [(2, 5, 8), (1, 1, 4), (3, 7, 16)])
+def test_decode_oracle_vs_brute_force(BH, S, D):
+    args = rand_decode(BH, S, D, seed=BH * 100 + S)
+    ref = brute_decode(*args)
+    np.testing.assert_allclose(O.decode_attention(*args), ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(C.decode_attention(*args), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_oracle_vs_torch_sdpa():
+    # an independent library routine on the dequantized operands
+    Q, K, V, sQ, sK, sV = rand_decode(6, 300, 64, seed=4)
+    qd = torch.from_numpy(Q.astype(np.float64) * sQ[:, None])[:, None, None, :]
+    kd = torch.from_numpy(K.astype(np.float64) * sK[..., None])[:, None]
+    vd = torch.from_numpy(V.astype(np.float64) * sV[..., None])[:, None]
+    ref = F.scaled_dot_product_attention(qd, kd, vd).reshape(6, 64).numpy()
+    np.testing.assert_allclose(O.decode_attention(Q, K, V, sQ, sK, sV), ref, atol=1e-12)
+    np.testing.assert_allclose(C.decode_attention(Q, K, V, sQ, sK, sV), ref, atol=1e-12)
+
+
+def test_decode_oracle_closed_forms():
+    Q, K, V, sQ, sK, sV = rand_decode(3, 1, 32, seed=5)
+    out = C.decode_attention(Q, K, V, sQ, sK, sV)           # S=1 -> V row
+    np.testing.assert_allclose(out, V[:, 0].astype(np.float64) * sV[:, :1], atol=1e-12)
+    Q, K, V, sQ, sK, sV = rand_decode(3, 50, 32, seed=6)
+    K[:] = K[:, :1]
+    sK[:] = sK[:, :1]                                        # constant keys -> mean of V
+    out = C.decode_attention(Q, K, V, sQ, sK, sV)
+    np.testing.assert_allclose(out, (V.astype(np.float64) * sV[..., None]).mean(1), atol=1e-12)
+    Q, K, V, sQ, sK, sV = rand_decode(2, 40, 16, seed=7)
+    perm = rng(8).permutation(40)                            # permutation invariance
+    a = C.decode_attention(Q, K, V, sQ, sK, sV)
+    b = C.decode_attention(Q, K[:, perm], V[:, perm], sQ, sK[:, perm], sV[:, perm])
+    np.testing.assert_allclose(a, b, atol=1e-12)
+
+
+def brute_prefill(Q, K, V, sQ, sK, sV, causal):
+    BH, S, D = Q.shape
+    out = np.zeros((BH, S, D))
+    for b in range(BH):
+        for i in range(S):
+            n = i + 1 if causal else S
+            sc = [sum(int(Q[b, i, d]) * int(K[b, j, d]) for d in range(D)) * float(sQ[b, i])
+                  * float(sK[b, j]) / math.sqrt(D) for j in range(n)]
+            m = max(sc)
+            p = [math.exp(x - m) for x in sc]
+            z = sum(p)
+            for d in range(D):
+                out[b, i, d] = sum(p[j] * float(V[b, j, d]) * float(sV[b, j])
+                                   for j in range(n)) / z
+    return out
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_oracle_vs_brute_force(causal):
+    g = rng(9)
+    Q, sQ = O.quantize_per_token(g.standard_normal((2, 6, 8)).astype(np.float32))
+    K, sK = O.quantize_per_token(g.standard_normal((2, 6, 8)).astype(np.float32))
+    V, sV = O.quantize_per_token(g.standard_normal((2, 6, 8)).astype(np.float32))
+    ref = brute_prefill(Q, K, V, sQ, sK, sV, causal)
+    np.testing.assert_allclose(O.prefill_attention(Q, K, V, sQ, sK, sV, causal), ref, atol=1e-12)
+    np.testing.assert_allclose(C.prefill_attention(Q, K, V, sQ, sK, sV, causal), ref, atol=1e-12)
+    if causal:  # row 0 sees only key 0
+        np.testing.assert_allclose(ref[:, 0], V[:, 0] * sV[:, :1], atol=1e-12)
+
+
+def test_prefill_oracle_vs_torch_sdpa():
+    g = rng(10)
+    Q, sQ = O.quantize_per_token(g.standard_normal((3, 40, 32)).astype(np.float32))
+    K, sK = O.quantize_per_token(g.standard_normal((3, 40, 32)).astype(np.float32))
+    V, sV = O.quantize_per_token(g.standard_normal((3, 40, 32)).astype(np.float32))
+    deq = lambda a, s: torch.from_numpy(a.astype(np.float64) * s[..., None].astype(np.float64))
+    for causal in (False, True):
+        ref = F.scaled_dot_product_attention(deq(Q, sQ), deq(K, sK), deq(V, sV),
+                                             is_causal=causal).numpy()
+        np.testing.assert_allclose(C.prefill_attention(Q, K, V, sQ, sK, sV, causal), ref,
+                                   atol=1e-12)
+
+
+# ---------------------------------------------------------------- GEMM / MLP
+
+def test_gemm_vs_triple_loop_and_extremes():
+    g = rng(11)
+    A = g.integers(-128, 128, (5, 7)).astype(np.int8)
+    B = g.integers(-128, 128, (7, 3)).astype(np.int8)
+    ref = np.array([[sum(int(A[m, k]) * int(B[k, n]) for k in range(7)) for n in range(3)]
+                    for m in range(5)])
+    np.testing.assert_array_equal(O.gemm_i8_i32(A, B), ref)
+    np.testing.assert_array_equal(C.gemm_i8_i32(A, B), ref)
+    A = np.full((2, 16384), -128, np.int8)   # largest reduction of the MLP config
+    B = np.full((16384, 2), -128, np.int8)
+    np.testing.assert_array_equal(C.gemm_i8_i32(A, B), 16384 * 128 * 128)
+    I = np.eye(8, dtype=np.int8)             # identity / transpose sanity
+    X = g.integers(-128, 128, (8, 8)).astype(np.int8)
+    np.testing.assert_array_equal(C.gemm_i8_i32(X, I), X)
+    np.testing.assert_array_equal(C.gemm_i8_i32(I, X), X)
+    with pytest.raises(OverflowError):
+        C.gemm_i8_i32(np.full((1, 140000), -128, np.int8), np.full((140000, 1), -128, np.int8))
+
+
+def test_gemm_c_matches_numpy_random():
+    g = rng(12)
+    A = g.integers(-128, 128, (64, 200)).astype(np.int8)
+    B = g.integers(-128, 128, (200, 96)).astype(np.int8)
+    np.testing.assert_array_equal(C.gemm_i8_i32(A, B), O.gemm_i8_i32(A, B))
+
+
+def test_gelu_closed_form_and_torch():
+    x = np.array([0.0, 1.0, -1.0, 3.0, -3.0, 10.0, -10.0], np.float32)
+    y = O.gelu_tanh_f32(x)
+    assert y[0] == 0.0 and abs(y[5] - 10.0) < 1e-6 and abs(y[6]) < 1e-6
+    # closed form at 1: 0.5*(1+tanh(sqrt(2/pi)*(1+0.044715)))
+    assert abs(y[1] - 0.5 * (1 + math.tanh(math.sqrt(2 / math.pi) * 1.044715))) < 1e-6
+    xs = rng(13).standard_normal(10000).astype(np.float32) * 4
+    ref = F.gelu(torch.from_numpy(xs), approximate="tanh").numpy()
+    np.testing.assert_allclose(O.gelu_tanh_f32(xs), ref, rtol=2e-6, atol=2e-7)
+
+
+def _mlp_inputs(T, dm, dff, seed):
+    g = rng(seed)
+    x, sx = O.quantize_per_token(g.standard_normal((T, dm)).astype(np.float32))
+    W1, s1 = O.quantize_per_channel_w((g.standard_normal((dm, dff)) * 0.02).astype(np.float32))
+    W2, s2 = O.quantize_per_channel_w((g.standard_normal((dff, dm)) * 0.02).astype(np.float32))
+    return x, W1, W2, sx, s1, s2
+
+
+def test_mlp_stages_restate_reference_order():
+    x, W1, W2, sx, s1, s2 = _mlp_inputs(16, 64, 128, seed=14)
+    out, osc, st = O.mlp_forward(x, W1, W2, sx, s1, s2, return_stages=True)
+    # stage 1: exact accumulators, then ((acc*sx)*sW1) in fp32, GELU
+    np.testing.assert_array_equal(st["acc1"], C.gemm_i8_i32(x, W1))
+    v = O.gelu_tanh_f32((st["acc1"].astype(np.float32) * sx[:, None]) * s1[None, :])
+    np.testing.assert_array_equal(st["v"], v)
+    # the hidden row absmax is taken before fp16 rounding
+    np.testing.assert_array_equal(st["h_amax"], np.abs(v).max(1))
+    # requant: every code is within half a step of h16/sh (rounding), sh = amax/127
+    np.testing.assert_allclose(st["sh"], st["h_amax"] / np.float32(127), rtol=1e-7)
+    recon = st["hq"].astype(np.float64) * st["sh"][:, None]
+    assert (np.abs(recon - st["h16"].astype(np.float64)) <= st["sh"][:, None] * 0.5001).all()
+    assert np.abs(st["hq"]).max() == 127
+    np.testing.assert_array_equal(st["acc2"], C.gemm_i8_i32(st["hq"], W2))
+    # per-token output codes use the full range in every row
+    assert (np.abs(out.astype(np.int32)).max(1) == 127).all()
+    deq = out.astype(np.float64) * osc[:, None]
+    ref = O.mlp_dequant_reference(x, W1, W2, sx, s1, s2)
+    cos = (deq * ref).sum() / np.linalg.norm(deq) / np.linalg.norm(ref)
+    assert cos > 0.999
+
+
+def test_mlp_kats_zero_and_constant():
+    T, dm, dff = 8, 32, 64
+    z8 = np.zeros((T, dm), np.int8)
+    out, osc = O.mlp_forward(z8, np.zeros((dm, dff), np.int8), np.zeros((dff, dm), np.int8),
+                             np.full(T, 1e-8 / 127, np.float32), np.full(dff, 1e-8 / 127, np.float32),
+                             np.full(dm, 1e-8 / 127, np.float32))
+    np.testing.assert_array_equal(out, 0)
+    # constant dataset (validation/generate_test_data.py:320-336): one code everywhere
+    x, sx = O.quantize_per_token(np.ones((T, dm), np.float32))
+    W1, s1 = O.quantize_per_channel_w(np.full((dm, dff), 0.01, np.float32))
+    W2, s2 = O.quantize_per_channel_w(np.full((dff, dm), 0.01, np.float32))
+    out, osc = O.mlp_forward(x, W1, W2, sx, s1, s2)
+    np.testing.assert_array_equal(out, 127)
+
+
+def test_mlp_per_tensor_output_path():
+    x, W1, W2, _, _, _ = _mlp_inputs(16, 64, 128, seed=15)
+    out, osc = O.mlp_forward(x, W1, W2, np.float32(0.01), np.float32(0.002),
+                             np.float32(0.003), per_token_out=False)
+    assert np.ndim(osc) == 0 and np.abs(out.astype(np.int32)).max() == 127
+
+
+# ---------------------------------------------------------------- quant utils
+
+def test_quant_utils_per_tensor():
+    x = np.array([0.0, 1.0, -2.0, 0.5, 65504.0], np.float16)
+    q, s = O.quantize_fp16_per_tensor(x)
+    assert s == np.float32(np.float32(65504.0) / np.float32(127.0))
+    assert q[4] == 127 and q[0] == 0
+    q0, s0 = O.quantize_fp16_per_tensor(np.zeros(16, np.float16))
+    np.testing.assert_array_equal(q0, 0)  # the 1e-8 guard (reference returns -128 here)
+    d = O.dequantize_int8_to_fp16(np.array([-128, 0, 127], np.int8), np.float32(0.5))
+    np.testing.assert_array_equal(d, np.array([-64.0, 0.0, 63.5], np.float16))
