@@ -52,6 +52,36 @@ def time_steps(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+def calibrate(dev):
+    """On-box ceilings: non-temporal chunked streaming read, vector copy, i8 MFMA."""
+    import ctypes
+
+    import torch
+
+    L = ctypes.CDLL(os.path.join(PKG_DIR, "libint8k_calib.so"))
+    stream = torch.cuda.current_stream(dev)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    nbytes = 4 << 30
+    buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.empty(1 << 22, dtype=torch.int32, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    ms = time_steps(lambda: L.int8k_calib_stream_chunk_nt(P(buf), ctypes.c_size_t(nbytes),
+                                                          P(sink), 4096, st), 10, 2, stream)
+    read_tbs = nbytes / (ms * 1e-3) / 1e12
+    half = nbytes // 2
+    ms = time_steps(lambda: L.int8k_calib_copy(P(buf), ctypes.c_void_p(buf.data_ptr() + half),
+                                               ctypes.c_size_t(half), 8192, st), 10, 2, stream)
+    copy_tbs = 2 * half / (ms * 1e-3) / 1e12
+    blocks, iters = 4096, 2000
+    ms = time_steps(lambda: L.int8k_calib_mfma_i8(blocks, iters, P(sink), st), 5, 1, stream)
+    mfma_tops = blocks * 4 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
+    del buf
+    torch.cuda.empty_cache()
+    return {"hbm_stream_read_TBps": round(read_tbs, 3), "hbm_copy_rw_TBps": round(copy_tbs, 3),
+            "mfma_i8_16x16x64_TOPS": round(mfma_tops, 1),
+            "copy_kernel_bytes": {"read": half, "write": half}}
+
+
 def cpu_baseline_decode(case, B, H, D, S, budget_s=12.0):
     """Time the C oracle (all host cores) on a growing sample of (b,h) heads."""
     import numpy as np
@@ -84,6 +114,16 @@ def cpu_baseline_decode(case, B, H, D, S, budget_s=12.0):
                 seconds=spent, heads=heads)
 
 
+def measured_traffic(key):
+    """HBM bytes per launch of the dominant kernel, from the committed PMC summary."""
+    try:
+        with open(os.path.join(REPO_DIR, "profiles", "traffic.json")) as f:
+            t = json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+    return None if t is None else int(t["read_bytes"]) + int(t["write_bytes"])
+
+
 def bench_decode(args):
     import torch
 
@@ -93,6 +133,9 @@ def bench_decode(args):
     B, H, D, S = args.batch, args.heads, args.head_dim, args.ctx
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    ceilings = None if args.no_calibrate else calibrate(dev)
+    if ceilings:
+        log(f"[bench] on-box ceilings: {ceilings}")
     log(f"[bench] generating decode inputs B{B} H{H} D{D} S{S} (outliers 1% x8)")
     case = workloads.decode_case(B, H, D, S, seed=args.seed, outlier_frac=0.01, device=dev)
     BH = B * H
@@ -151,8 +194,11 @@ def bench_decode(args):
                    "kv_bytes": kv_bytes, "scale_bytes": scale_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "decode_split_kernel + decode_combine_kernel (one step)"},
+                     "traffic": measured_traffic(f"decode_b{B}h{H}d{D}_s{S}"),
+                     "kernel": "decode_split_kernel + decode_combine_kernel (one step)",
+                     "measured_ceiling": (round(ceilings["hbm_stream_read_TBps"] * 1e3, 1)
+                                          if ceilings else None)},
+        "ceilings": ceilings,
     }
     if not args.no_cpu_baseline:
         cb = cpu_baseline_decode(case, B, H, D, S, budget_s=args.cpu_budget)
@@ -177,6 +223,7 @@ def main():
     ap.add_argument("--nsplit", type=int, default=0)
     ap.add_argument("--seed", type=int, default=20241201)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-calibrate", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -28,6 +28,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 LIB_NAME = "libint8k.so"
+CALIB_LIB_NAME = "libint8k_calib.so"
 EXT_NAME = "int8_ext"
 
 HIP_SOURCES = ["status.hip", "decode.hip"]
@@ -93,6 +94,16 @@ def build_lib(force: bool = False) -> str:
     return out
 
 
+def build_calib(force: bool = False) -> str:
+    """Roofline calibration kernels (bench only), a library of their own."""
+    src = os.path.join(CSRC, "calib.hip")
+    out = os.path.join(PKG_DIR, CALIB_LIB_NAME)
+    if force or _newer(out, [src]):
+        _run([HIPCC, *HIP_FLAGS, "-shared", src, "-o", out + ".tmp"])
+        os.replace(out + ".tmp", out)
+    return out
+
+
 def build_ext(force: bool = False) -> str:
     import torch  # noqa: F401  (headers and libraries of the installed torch)
     from torch.utils import cpp_extension
@@ -121,6 +132,7 @@ def build_ext(force: bool = False) -> str:
 
 def build(force: bool = False) -> None:
     build_lib(force)
+    build_calib(force)
     build_ext(force)
 
 
@@ -130,6 +142,7 @@ if __name__ == "__main__":
     ap.add_argument("--lib-only", action="store_true")
     args = ap.parse_args()
     build_lib(args.force)
+    build_calib(args.force)
     if not args.lib_only:
         build_ext(args.force)
     print("built:", lib_path(), "" if args.lib_only else ext_path())

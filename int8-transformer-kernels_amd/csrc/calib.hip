@@ -1,0 +1,107 @@
+// calib.hip — on-box ceilings for the roofline (built into libint8k_calib.so,
+// used by bench.py only; not part of the C ABI of the kernels).
+//
+//   int8k_calib_stream_read : every lane streams 16-byte vectors through the
+//       buffer (grid-stride), folds them with XOR and writes one word per
+//       thread, so the HBM read bandwidth ceiling is bytes / time.
+//   int8k_calib_copy        : plain 16-byte vector copy; its FETCH_SIZE /
+//       WRITE_SIZE counters calibrate the PMC byte counts of other kernels.
+//   int8k_calib_mfma_i8     : back-to-back v_mfma_i32_16x16x64_i8 on
+//       independent accumulators, no memory traffic, giving the dense INT8
+//       MFMA ceiling as 2*16*16*64 ops per instruction.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void calib_stream_read_kernel(const int4* __restrict__ src,
+                                                                size_t n_vec,
+                                                                int* __restrict__ sink) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    int acc = 0;
+    size_t i = tid;
+    for (; i + 3 * stride < n_vec; i += 4 * stride) {
+        const int4 a = src[i], b = src[i + stride], c = src[i + 2 * stride],
+                   d = src[i + 3 * stride];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^
+               d.z ^ d.w;
+    }
+    for (; i < n_vec; i += stride) {
+        const int4 a = src[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    sink[tid] = acc;
+}
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// Each wave streams its own contiguous chunk with 8 x 1 KiB loads in flight,
+// non-temporal (the access pattern of the decode kernel's K/V stream).
+__global__ __launch_bounds__(256) void calib_stream_chunk_nt_kernel(const v4i_t* __restrict__ src,
+                                                                    size_t vec_per_wave,
+                                                                    int* __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const v4i_t* p = src + wave * vec_per_wave + lane;
+    int acc = 0;
+    for (size_t i = 0; i + 8 * 64 <= vec_per_wave; i += 8 * 64) {
+        v4i_t v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = __builtin_nontemporal_load(p + i + t * 64);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc ^= v[t].x ^ v[t].y ^ v[t].z ^ v[t].w;
+    }
+    sink[wave * 64 + lane] = acc;
+}
+
+__global__ __launch_bounds__(256) void calib_copy_kernel(const int4* __restrict__ src,
+                                                         int4* __restrict__ dst, size_t n_vec) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_vec; i += stride)
+        dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void calib_mfma_i8_kernel(int iters, int* __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v4i a = {lane, lane + 1, lane + 2, lane + 3};
+    v4i b = {lane ^ 5, lane ^ 9, lane ^ 3, lane ^ 7};
+    v4i c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+    for (int it = 0; it < iters; ++it) {
+        c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c3, 0, 0, 0);
+    }
+    const v4i s = c0 + c1 + c2 + c3;
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s.x ^ s.y ^ s.z ^ s.w;
+}
+
+extern "C" int int8k_calib_stream_read(const void* buf, size_t bytes, int* sink, int blocks,
+                                       void* stream) {
+    calib_stream_read_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+        (const int4*)buf, bytes / 16, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// bytes must be a multiple of waves * 8 KiB; waves a multiple of 4.
+extern "C" int int8k_calib_stream_chunk_nt(const void* buf, size_t bytes, int* sink, int waves,
+                                           void* stream) {
+    const size_t vec_per_wave = bytes / 16 / (size_t)waves;
+    calib_stream_chunk_nt_kernel<<<waves / 4, 256, 0, (hipStream_t)stream>>>(
+        (const v4i_t*)buf, vec_per_wave, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+extern "C" int int8k_calib_copy(const void* src, void* dst, size_t bytes, int blocks,
+                                void* stream) {
+    calib_copy_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>((const int4*)src, (int4*)dst,
+                                                               bytes / 16);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// ops per launch = blocks * 4 waves * iters * 4 MFMAs * 32768
+extern "C" int int8k_calib_mfma_i8(int blocks, int iters, int* sink, void* stream) {
+    calib_mfma_i8_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(iters, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}

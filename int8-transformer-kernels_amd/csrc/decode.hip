@@ -39,46 +39,75 @@ namespace int8k {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
+constexpr int kNtKV = 1;      // non-temporal K/V loads (each row is read once)
+constexpr int kNtScales = 2;  // non-temporal sK/sV loads
 constexpr int kBlockThreads = 64 * kWavesPerBlock;
-constexpr int kSlots = 8;  // rows per row-group per wave iteration
 
-template <int D>
+// NS = load slots: rows per row-group per wave iteration (each slot is one
+// 16-byte K load and one 16-byte V load per lane).
+template <int D, int NS>
 struct DecodeGeom {
     static_assert(D == 64 || D == 128, "decode supports head_dim 64 and 128");
+    static_assert(NS == 4 || NS == 8, "slots per iteration: 4 or 8");
     static constexpr int kLanesPerRow = D / 16;
     static constexpr int kGroups = 64 / kLanesPerRow;
-    static constexpr int kRowsPerIter = kGroups * kSlots;
+    static constexpr int kRowsPerIter = kGroups * NS;
 };
 
 // Rows per wave iteration for a head dim (host side).
-inline int rows_per_iter(int D) { return (64 / (D / 16)) * kSlots; }
+inline int rows_per_iter(int D, int ns) { return (64 / (D / 16)) * ns; }
+
+// Launch-time tuning of the decode kernel.
+struct DecodeTuning {
+    int slots;         // NS
+    int flags;         // kNtKV | kNtScales
+    int target_units;  // units (waves) to aim for
+    int stagger;       // rotate each unit's starting iteration
+};
 
 struct SplitPlan {
     int nsplit;
     int chunk;
 };
 
-inline int env_target_units() {
-    static const int v = [] {
-        const char* e = std::getenv("INT8K_DECODE_TARGET_UNITS");
-        const int x = e ? std::atoi(e) : 0;
-        return x > 0 ? x : 0;
-    }();
-    return v;
+inline int env_int(const char* name, int dflt) {
+    const char* e = std::getenv(name);
+    return e ? std::atoi(e) : dflt;
 }
 
-// Split-count choice.  A unit is one wave; 256 CUs hold 2048 waves at the
-// kernel's occupancy (8 waves/CU), so aim for ~4 units per wave slot to keep
-// the tail short while each chunk still spans several loop iterations.
+// Defaults measured on MI355X at the BASELINE shapes (B32 H32 D128 8K and
+// B8 H32 D64 32K): D=128 — 8 slots, non-temporal K/V loads, ~8192 units (two
+// resident rounds at 16 waves/CU); D=64 — 4 slots, non-temporal scale loads,
+// ~1024 longer units.  Both rotate each unit's starting iteration (stagger),
+// which was worth 2-5%.  The INT8K_DECODE_* variables override these for
+// tuning sweeps (read once per process).
+DecodeTuning tuning_for(int D) {
+    static const int e_slots = env_int("INT8K_DECODE_SLOTS", 0);
+    static const int e_flags = env_int("INT8K_DECODE_FLAGS", -1);
+    static const int e_units = env_int("INT8K_DECODE_TARGET_UNITS", 0);
+    static const int e_stagger = env_int("INT8K_DECODE_STAGGER", -1);
+    DecodeTuning t;
+    if (D == 128) t = DecodeTuning{8, kNtKV, 8192, 1};
+    else t = DecodeTuning{4, kNtScales, 1024, 1};
+    if (e_slots == 4 || e_slots == 8) t.slots = e_slots;
+    if (e_flags >= 0) t.flags = e_flags & 3;
+    if (e_units > 0) t.target_units = e_units;
+    if (e_stagger >= 0) t.stagger = e_stagger;
+    return t;
+}
+
+// Split-count choice: a unit is one wave over one KV chunk of one (b,h);
+// aim for tuning.target_units units in total, each chunk a multiple of the
+// rows one wave iteration covers.
 SplitPlan plan_splits(int BH, int S, int D, int nsplit_req) {
-    const int R = rows_per_iter(D);
+    const DecodeTuning tn = tuning_for(D);
+    const int R = rows_per_iter(D, tn.slots);
     const long long max_split = ceil_div(S, R);
     long long ns;
     if (nsplit_req > 0) {
         ns = nsplit_req;
     } else {
-        const int target = env_target_units() > 0 ? env_target_units() : 8192;
-        ns = ceil_div(target, BH);
+        ns = ceil_div(tn.target_units, BH);
         // keep at least 4 iterations per unit unless S is short
         const long long by_len = std::max<long long>(1, ceil_div(S, 4LL * R));
         ns = std::min(ns, by_len);
@@ -98,6 +127,23 @@ __device__ __forceinline__ Int4 load16(const int8_t* p) {
     return Int4{v.x, v.y, v.z, v.w};
 }
 
+template <bool NT>
+__device__ __forceinline__ float load_f32(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+template <bool NT>
+__device__ __forceinline__ Int4 load_kv16(const int8_t* p) {
+    if constexpr (NT) {
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+        return Int4{v.x, v.y, v.z, v.w};
+    } else {
+        return load16(p);
+    }
+}
+
 __device__ __forceinline__ void fma_bytes(float* acc, int word, float w) {
     acc[0] = fmaf(w, sbyte_to_f32<0>(word), acc[0]);
     acc[1] = fmaf(w, sbyte_to_f32<1>(word), acc[1]);
@@ -107,20 +153,19 @@ __device__ __forceinline__ void fma_bytes(float* acc, int word, float w) {
 
 template <int D>
 __device__ __forceinline__ int group_sum(int v) {
-    if constexpr (DecodeGeom<D>::kLanesPerRow == 8) return group8_sum(v);
+    if constexpr (D == 128) return group8_sum(v);
     else return group4_sum(v);
 }
 
 // One wave iteration over NSLOT rows per group.  MASKED handles the last
 // partial block of a chunk: rows >= j1 get score -inf and weight 0 (their
 // loads are redirected to row j1-1, which is in bounds).
-template <int D, bool MASKED, bool VEC_SCALES>
+template <int D, int NS, bool MASKED, bool VEC_SCALES, int FL>
 __device__ __forceinline__ void decode_iter(
     const int8_t* __restrict__ Kbh, const int8_t* __restrict__ Vbh,
     const float* __restrict__ sKbh, const float* __restrict__ sVbh,
     int row0, int j1, int sub, const Int4& q, float qscale,
     float& m, float& l, float* acc) {
-    constexpr int NS = kSlots;
     Int4 kv[NS], vv[NS];
     float sk[NS], sv[NS];
 
@@ -128,29 +173,39 @@ __device__ __forceinline__ void decode_iter(
         const int8_t* kp = Kbh + (size_t)row0 * D + sub * 16;
         const int8_t* vp = Vbh + (size_t)row0 * D + sub * 16;
 #pragma unroll
-        for (int t = 0; t < NS; ++t) kv[t] = load16(kp + t * D);
+        for (int t = 0; t < NS; ++t) kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * D);
 #pragma unroll
-        for (int t = 0; t < NS; ++t) vv[t] = load16(vp + t * D);
+        for (int t = 0; t < NS; ++t) vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * D);
         if constexpr (VEC_SCALES) {
 #pragma unroll
             for (int t = 0; t < NS; t += 4) {
-                const float4 a = *reinterpret_cast<const float4*>(sKbh + row0 + t);
-                const float4 b = *reinterpret_cast<const float4*>(sVbh + row0 + t);
+                typedef float v4f __attribute__((ext_vector_type(4)));
+                v4f a, b;
+                if constexpr ((FL & kNtScales) != 0) {
+                    a = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sKbh + row0 + t));
+                    b = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sVbh + row0 + t));
+                } else {
+                    a = *reinterpret_cast<const v4f*>(sKbh + row0 + t);
+                    b = *reinterpret_cast<const v4f*>(sVbh + row0 + t);
+                }
                 sk[t] = a.x; sk[t + 1] = a.y; sk[t + 2] = a.z; sk[t + 3] = a.w;
                 sv[t] = b.x; sv[t + 1] = b.y; sv[t + 2] = b.z; sv[t + 3] = b.w;
             }
         } else {
 #pragma unroll
-            for (int t = 0; t < NS; ++t) { sk[t] = sKbh[row0 + t]; sv[t] = sVbh[row0 + t]; }
+            for (int t = 0; t < NS; ++t) {
+                sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + row0 + t);
+                sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + row0 + t);
+            }
         }
     } else {
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
             const int r = min(row0 + t, j1 - 1);
-            kv[t] = load16(Kbh + (size_t)r * D + sub * 16);
-            vv[t] = load16(Vbh + (size_t)r * D + sub * 16);
-            sk[t] = sKbh[r];
-            sv[t] = sVbh[r];
+            kv[t] = load_kv16<(FL & kNtKV) != 0>(Kbh + (size_t)r * D + sub * 16);
+            vv[t] = load_kv16<(FL & kNtKV) != 0>(Vbh + (size_t)r * D + sub * 16);
+            sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + r);
+            sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + r);
         }
     }
 
@@ -195,15 +250,16 @@ __device__ __forceinline__ void decode_iter(
     m = m_new;
 }
 
-// Pass 1: one wave per (bh, split); writes the unnormalised partial state.
-template <int D, bool VEC_SCALES>
+// Pass 1: one wave per (bh, split); writes the unnormalised partial state,
+// or — when the KV sequence is not split (FINAL) — the fp16 output itself.
+template <int D, int NS, bool VEC_SCALES, bool FINAL, int FL>
 __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K,
     const int8_t* __restrict__ V, const float* __restrict__ sQ,
     const float* __restrict__ sK, const float* __restrict__ sV,
-    float* __restrict__ part_ml, float* __restrict__ part_acc,
-    int S, int nsplit, int chunk, int units, float qk_scale_log2) {
-    using G = DecodeGeom<D>;
+    float* __restrict__ part_ml, float* __restrict__ part_acc, uint16_t* __restrict__ out,
+    int S, int nsplit, int chunk, int units, float qk_scale_log2, int stagger) {
+    using G = DecodeGeom<D, NS>;
     const int lane = threadIdx.x & 63;
     const int unit = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     if (unit >= units) return;  // whole wave exits; no block barrier below
@@ -228,13 +284,20 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 
-    int base = j0;
-    for (; base + G::kRowsPerIter <= j1; base += G::kRowsPerIter)
-        decode_iter<D, false, VEC_SCALES>(Kbh, Vbh, sKbh, sVbh, base + grp * kSlots, j1, sub,
-                                          q, qscale, m, l, acc);
+    // Full iterations, optionally started at a unit-dependent rotation so that
+    // concurrent waves do not walk identical address offsets in lockstep.
+    const int n_full = (j1 - j0) / G::kRowsPerIter;
+    int it = stagger ? (int)(((unsigned)unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
+    for (int k = 0; k < n_full; ++k) {
+        decode_iter<D, NS, false, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh,
+                                                  j0 + it * G::kRowsPerIter + grp * NS, j1, sub,
+                                                  q, qscale, m, l, acc);
+        it = (it + 1 == n_full) ? 0 : it + 1;
+    }
+    const int base = j0 + n_full * G::kRowsPerIter;
     if (base < j1)
-        decode_iter<D, true, VEC_SCALES>(Kbh, Vbh, sKbh, sVbh, base + grp * kSlots, j1, sub,
-                                         q, qscale, m, l, acc);
+        decode_iter<D, NS, true, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, base + grp * NS, j1, sub,
+                                                 q, qscale, m, l, acc);
 
     // Merge the G row-group states of this wave (lanes with equal `sub`).
     float M = m;
@@ -249,6 +312,20 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
         L += __shfl_xor(L, off);
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
+    }
+    if constexpr (FINAL) {
+        if (grp == 0) {
+            const float inv = 1.f / L;
+            uint16_t h[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) h[e] = f32_to_f16_bits(acc[e] * inv);
+            uint4* dst = reinterpret_cast<uint4*>(out + (size_t)unit * D + sub * 16);
+            dst[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                h[6] | (h[7] << 16));
+            dst[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16),
+                                h[12] | (h[13] << 16), h[14] | (h[15] << 16));
+        }
+        return;
     }
     if (grp == 0) {
         float4* dst = reinterpret_cast<float4*>(part_acc + (size_t)unit * D + sub * 16);
@@ -314,6 +391,37 @@ DecodeWorkspace carve(void* ws, long long units, int D) {
                            ml_bytes + acc_bytes};
 }
 
+template <int D, int NS, bool VEC, bool FINAL>
+void launch_split(int flags, int stagger, dim3 grid, hipStream_t stream, const int8_t* Q,
+                  const int8_t* K, const int8_t* V, const float* sQ, const float* sK,
+                  const float* sV, const DecodeWorkspace& w, uint16_t* out, int S,
+                  const SplitPlan& plan, int units, float qk) {
+#define INT8K_SPLIT_LAUNCH(FLV)                                                               \
+    decode_split_kernel<D, NS, VEC, FINAL, FLV><<<grid, kBlockThreads, 0, stream>>>(          \
+        Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, out, S, plan.nsplit, plan.chunk, units, qk, \
+        stagger)
+    switch (flags & 3) {
+        case 0: INT8K_SPLIT_LAUNCH(0); break;
+        case 1: INT8K_SPLIT_LAUNCH(1); break;
+        case 2: INT8K_SPLIT_LAUNCH(2); break;
+        default: INT8K_SPLIT_LAUNCH(3); break;
+    }
+#undef INT8K_SPLIT_LAUNCH
+}
+
+template <int D, bool VEC, bool FINAL>
+void launch_split_ns(int ns, int flags, int stagger, dim3 grid, hipStream_t stream,
+                     const int8_t* Q, const int8_t* K, const int8_t* V, const float* sQ,
+                     const float* sK, const float* sV, const DecodeWorkspace& w, uint16_t* out,
+                     int S, const SplitPlan& plan, int units, float qk) {
+    if (ns == 4)
+        launch_split<D, 4, VEC, FINAL>(flags, stagger, grid, stream, Q, K, V, sQ, sK, sV, w, out,
+                                       S, plan, units, qk);
+    else
+        launch_split<D, 8, VEC, FINAL>(flags, stagger, grid, stream, Q, K, V, sQ, sK, sV, w, out,
+                                       S, plan, units, qk);
+}
+
 template <int D>
 int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
                   const float* sQ, const float* sK, const float* sV, int BH, int S,
@@ -321,17 +429,24 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     const long long units = (long long)BH * plan.nsplit;
     const float qk_scale_log2 = (1.0f / std::sqrt((float)D)) * kLog2e;
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
-    const bool vec_scales = (S % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
-    if (vec_scales)
-        decode_split_kernel<D, true><<<grid, kBlockThreads, 0, stream>>>(
-            Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, S, plan.nsplit, plan.chunk, (int)units,
-            qk_scale_log2);
+    const bool vec = (S % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
+    const DecodeTuning tn = tuning_for(D);
+    const int ns = tn.slots;
+    const int fl = tn.flags;
+    const int sg = tn.stagger;
+    const int u = (int)units;
+    const float qk = qk_scale_log2;
+    const bool final_pass = plan.nsplit == 1 && aligned_to(out, 16);
+    if (vec && final_pass)
+        launch_split_ns<D, true, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
+    else if (vec)
+        launch_split_ns<D, true, false>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
+    else if (final_pass)
+        launch_split_ns<D, false, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
     else
-        decode_split_kernel<D, false><<<grid, kBlockThreads, 0, stream>>>(
-            Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, S, plan.nsplit, plan.chunk, (int)units,
-            qk_scale_log2);
+        launch_split_ns<D, false, false>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
     int st = check_launch("decode_split_kernel");
-    if (st != INT8K_OK) return st;
+    if (st != INT8K_OK || final_pass) return st;
     const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));
     decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out, BH,
                                                                   plan.nsplit);
