@@ -77,6 +77,58 @@ int int8k_decode_attention_forward(
 /* The split count the forward call uses for this shape (after clamping). */
 int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
 
+/* ------------------------------------------------------------------------ */
+/* INT8 MLP: Linear -> GELU(tanh) -> Linear with dynamic per-token requant.  */
+/*                                                                          */
+/*   x  int8 [T, d_model]    W1 int8 [d_model, d_ff]   W2 int8 [d_ff, d_model]*/
+/*   (or, with INT8K_MLP_WEIGHTS_PREPACKED, W1T [d_ff, d_model] and          */
+/*    W2T [d_model, d_ff] from int8k_transpose_int8_weights)                 */
+/*   scale_x  [T] or [1]; scale_W1 [d_ff] or [1]; scale_W2 [d_model] or [1]   */
+/*   (n_scale_* gives the length; 1 broadcasts); bias1 [d_ff] fp32 or NULL,  */
+/*   added before GELU.                                                      */
+/*   out int8 [T, d_model]; out_scale fp32 [T] (per-token output) or [1]     */
+/*   with INT8K_MLP_OUT_PER_TENSOR.                                          */
+/*                                                                          */
+/* One entry point covers the reference's four MLP launchers                 */
+/* (declared at kernels/int8_ext.cu:39-68):                                  */
+/*   int8_mlp_forward            (kernels/int8_mlp.cu:1231-1240):            */
+/*       n_scale_* = 1, INT8K_MLP_OUT_PER_TENSOR;                            */
+/*   int8_mlp_forward_per_channel (kernels/int8_mlp.cu:1248-1258):           */
+/*       n_scale_x = T, n_scale_W1 = d_ff, n_scale_W2 = d_model;             */
+/*   int8_mlp_forward_per_channel_bias (kernels/int8_mlp.cu:1267-1279):      */
+/*       as above with bias1;                                                */
+/*   int8_mlp_forward_prepacked  (kernels/int8_mlp.cu:1304-1314):            */
+/*       INT8K_MLP_WEIGHTS_PREPACKED | INT8K_MLP_OUT_PER_TENSOR.             */
+/* int8_mlp_get_output_scale (kernels/int8_mlp.cu:1317-1322) has no          */
+/* counterpart: the scale is written to out_scale on the stream instead of   */
+/* being read back from a library global.                                    */
+/* d_model and d_ff must be multiples of 16; T is arbitrary.  x, W1, W2 must */
+/* be 16-byte aligned.                                                       */
+/* ------------------------------------------------------------------------ */
+#define INT8K_MLP_WEIGHTS_PREPACKED 1
+#define INT8K_MLP_OUT_PER_TENSOR 2
+
+size_t int8k_mlp_workspace_bytes(int T, int d_model, int d_ff, int flags);
+
+int int8k_mlp_forward(
+    const int8_t* x, const int8_t* W1, const int8_t* W2, int8_t* out,
+    const float* scale_x, int n_scale_x, const float* scale_W1, int n_scale_W1,
+    const float* scale_W2, int n_scale_W2, const float* bias1, float* out_scale,
+    int T, int d_model, int d_ff, int flags,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* W1 [d_model, d_ff] -> W1T [d_ff, d_model]; W2 [d_ff, d_model] -> W2T     */
+/* [d_model, d_ff].  Replaces transpose_int8_weights                         */
+/* (kernels/int8_mlp.cu:1288-1297, declared kernels/int8_ext.cu:59-62).      */
+int int8k_transpose_int8_weights(const int8_t* W1, const int8_t* W2, int8_t* W1T, int8_t* W2T,
+                                 int d_model, int d_ff, void* stream);
+
+/* Raw C[M,N] = A[M,K] . Bt[N,K]^T with exact int32 accumulation (the MLP's */
+/* GEMM core, kernels/int8_mlp.cu:242-310, exposed so its accumulators can   */
+/* be checked bit-exactly).  K % 16 == 0; A, Bt 16-byte aligned.             */
+int int8k_gemm_i8_i32(const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,23 @@ __global__ __launch_bounds__(256) void calib_mfma_i8_kernel(int iters, int* __re
     sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s.x ^ s.y ^ s.z ^ s.w;
 }
 
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void calib_mfma_i8_32_kernel(int iters, int* __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v4i a = {lane, lane + 1, lane + 2, lane + 3};
+    v4i b = {lane ^ 5, lane ^ 9, lane ^ 3, lane ^ 7};
+    v16i_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int it = 0; it < iters; ++it) {
+        c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c3, 0, 0, 0);
+    }
+    const v16i_t s = c0 + c1 + c2 + c3;
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s[0] ^ s[5] ^ s[10] ^ s[15];
+}
+
 extern "C" int int8k_calib_stream_read(const void* buf, size_t bytes, int* sink, int blocks,
                                        void* stream) {
     calib_stream_read_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
@@ -97,6 +114,12 @@ extern "C" int int8k_calib_copy(const void* src, void* dst, size_t bytes, int bl
                                 void* stream) {
     calib_copy_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>((const int4*)src, (int4*)dst,
                                                                bytes / 16);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// ops per launch = blocks * 4 waves * iters * 4 MFMAs * 65536
+extern "C" int int8k_calib_mfma_i8_32(int blocks, int iters, int* sink, void* stream) {
+    calib_mfma_i8_32_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(iters, sink);
     return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

@@ -1,0 +1,250 @@
+// gemm_i8.h — int8 x int8 -> int32 GEMM core on gfx950 MFMA, with fused epilogues.
+//
+//   C[M,N] = A[M,K] . Bt[N,K]^T      (both operands K-contiguous, row-major)
+//
+// Block tile 256 x 256 x 128, 256 threads = 4 waves in a 2 x 2 grid, each wave
+// owning a 128 x 128 sub-tile as 4 x 4 v_mfma_i32_32x32x32_i8 accumulators
+// (256 accumulator registers per lane).  Operands are staged global -> VGPR ->
+// LDS (double-buffered, rows padded to 144 bytes so the 16-byte fragment
+// reads of consecutive rows spread over the banks); the next K-step's global loads are
+// in flight while the current one runs on the matrix cores.  Blocks are mapped
+// XCD-first (consecutive tiles share an XCD and its L2) and grouped along M.
+//
+// Internal header of libint8k (mlp.hip, prefill.hip).
+#pragma once
+
+#include "int8k_common.h"
+
+namespace int8k {
+namespace gemm {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int kThreads = 256;
+constexpr int WM = 128, WN = 128;           // wave tile
+constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
+constexpr int LDS_STRIDE = BK + 16;         // padded row, bytes
+constexpr int A_STAGE = BM * LDS_STRIDE;
+constexpr int B_STAGE = BN * LDS_STRIDE;
+constexpr int STAGE_BYTES = A_STAGE + B_STAGE;
+constexpr int LDS_BYTES = 2 * STAGE_BYTES;  // 147456 of gfx950's 160 KiB
+constexpr int kChunksPerRow = BK / 16;
+constexpr int kChunks = BM * kChunksPerRow / kThreads;  // 16-byte chunks per thread per operand
+constexpr int kNumXcd = 8;
+constexpr int kGroupM = 8;
+
+// Linear block id -> (tile_m, tile_n): XCD-contiguous ranges, grouped along M.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    const int xcd = bid % kNumXcd;
+    const int local = bid / kNumXcd;
+    const int base = total / kNumXcd, rem = total % kNumXcd;
+    const int tile = xcd * base + min(xcd, rem) + local;
+    const int per_group = kGroupM * tiles_n;
+    const int group = tile / per_group;
+    const int first_m = group * kGroupM;
+    const int gm = min(tiles_m - first_m, kGroupM);
+    const int in_group = tile - group * per_group;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
+struct Frag {
+    int4 a[kChunks];
+    int4 b[kChunks];
+};
+
+// Global -> registers for one K-step.  Chunk c (16 B) of a 256 x BK operand
+// tile: row c / (BK/16), bytes (c % (BK/16)) * 16.  Rows past the matrix and
+// K past the end read a clamped in-bounds address; store_stage zeroes them,
+// so the loads themselves are unconditional and their wait lands late.
+__device__ __forceinline__ void load_stage(Frag& f, const int8_t* __restrict__ A,
+                                           const int8_t* __restrict__ Bt, int M, int N, int K,
+                                           int lda, int ldb, int m0, int n0, int k0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        const int c = t + i * kThreads;
+        const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+        const int gk = min(k0 + kc, K - 16);
+        f.a[i] = *reinterpret_cast<const int4*>(A + (size_t)min(m0 + row, M - 1) * lda + gk);
+        f.b[i] = *reinterpret_cast<const int4*>(Bt + (size_t)min(n0 + row, N - 1) * ldb + gk);
+    }
+}
+
+// One chunk of each operand (index i of load_stage) — for interleaving.
+__device__ __forceinline__ int4 load_chunk(const int8_t* __restrict__ P, int rows, int K, int ld,
+                                           int r0, int k0, int i) {
+    const int c = threadIdx.x + i * kThreads;
+    const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+    const int gk = min(k0 + kc, K - 16);
+    return *reinterpret_cast<const int4*>(P + (size_t)min(r0 + row, rows - 1) * ld + gk);
+}
+
+template <bool EDGE>
+__device__ __forceinline__ void store_chunk(int4 v, char* lds_op, int rows, int K, int r0, int k0,
+                                            int i) {
+    const int c = threadIdx.x + i * kThreads;
+    const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+    if constexpr (EDGE) {
+        if (!(k0 + kc < K && r0 + row < rows)) v = make_int4(0, 0, 0, 0);
+    }
+    *reinterpret_cast<int4*>(lds_op + row * LDS_STRIDE + kc) = v;
+}
+
+__device__ __forceinline__ v4i read_frag(const char* stage, int off, int t, int slice) {
+    return *reinterpret_cast<const v4i*>(stage + off + t * 32 * LDS_STRIDE + slice * 32);
+}
+
+// Registers -> LDS.  EDGE zeroes the chunks that load_stage clamped.
+template <bool EDGE>
+__device__ __forceinline__ void store_stage(const Frag& f, char* lds, int M, int N, int K,
+                                            int m0, int n0, int k0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        const int c = t + i * kThreads;
+        const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+        int4 va = f.a[i], vb = f.b[i];
+        if constexpr (EDGE) {
+            const bool kok = k0 + kc < K;
+            if (!(kok && m0 + row < M)) va = make_int4(0, 0, 0, 0);
+            if (!(kok && n0 + row < N)) vb = make_int4(0, 0, 0, 0);
+        }
+        *reinterpret_cast<int4*>(lds + row * LDS_STRIDE + kc) = va;
+        *reinterpret_cast<int4*>(lds + A_STAGE + row * LDS_STRIDE + kc) = vb;
+    }
+}
+
+__device__ __forceinline__ void read_slice(v4i (&a)[TM], v4i (&b)[TN], const char* stage,
+                                           int a_off, int b_off, int slice) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+        a[i] = *reinterpret_cast<const v4i*>(stage + a_off + i * 32 * LDS_STRIDE + slice * 32);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+        b[j] = *reinterpret_cast<const v4i*>(stage + b_off + j * 32 * LDS_STRIDE + slice * 32);
+}
+
+__device__ __forceinline__ void mfma_slice(v16i (&acc)[TM][TN], const v4i (&a)[TM],
+                                           const v4i (&b)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+// Instruction classes for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100,
+              kSchedDsWrite = 0x200;
+
+// 8 LDS reads interleaved with the first 8 of 16 MFMAs.
+__device__ __forceinline__ void sched_reads_mfma() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+}
+
+// The MFMA main loop: acc[i][j] (32x32 tiles) of this wave's 128x128 sub-tile.
+//
+// With one wave per SIMD the wave stalls on every MFMA issue, so all other
+// work of a K-step is threaded between MFMAs (sched_group_barrier) instead of
+// being issued in bursts.  K-step kt computes on LDS buffer kt&1 in four
+// 32-wide k slices:
+//   slices 0, 1: LDS reads of slice s+1 between the MFMAs of slice s
+//   slice 2:     LDS reads of slice 3, the LDS writes of stage kt+1 (held in
+//                registers since step kt-1) and the global loads of stage
+//                kt+2, all between the MFMAs of slice 2
+//   slice 3:     8 MFMAs, the barrier, then the LDS reads of slice 0 of
+//                stage kt+1 between the last 8 MFMAs
+// Writing buffer (kt+1)&1 during step kt is safe: its last reads (step kt-1)
+// completed before step kt-1's barrier.  Past the end of K the loads clamp to
+// valid addresses and the writes land in the buffer nobody reads again.
+template <bool EDGE>
+__device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __restrict__ A,
+                                         const int8_t* __restrict__ Bt, int M, int N, int K,
+                                         int lda, int ldb, int m0, int n0, char* lds) {
+    static_assert(BK == 128, "the schedule below is written for 4 k-slices per stage");
+    static_assert(kChunks == 8, "the schedule below threads 16 loads and writes per step");
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int nk = (K + BK - 1) / BK;
+    // fragment read offsets inside a stage: row (l%32), 16-byte half (l/32)
+    const int a_off = (wm * WM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    const int b_off = A_STAGE + (wn * WN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    Frag f;
+    load_stage(f, A, Bt, M, N, K, lda, ldb, m0, n0, 0);
+    store_stage<EDGE>(f, lds, M, N, K, m0, n0, 0);
+    load_stage(f, A, Bt, M, N, K, lda, ldb, m0, n0, BK);
+    __syncthreads();
+    v4i a[2][TM], b[2][TN];
+    read_slice(a[0], b[0], lds, a_off, b_off, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const char* cur = lds + (kt & 1) * STAGE_BYTES;
+        char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
+        __builtin_amdgcn_sched_barrier(0);
+        read_slice(a[1], b[1], cur, a_off, b_off, 1);
+        mfma_slice(acc, a[0], b[0]);
+        sched_reads_mfma();
+        __builtin_amdgcn_sched_barrier(0);
+        read_slice(a[0], b[0], cur, a_off, b_off, 2);
+        mfma_slice(acc, a[1], b[1]);
+        sched_reads_mfma();
+        __builtin_amdgcn_sched_barrier(0);
+        // slice 2, one group per MFMA: a fragment read of slice 3, a chunk
+        // written to the next stage and its replacement load, then the MFMA
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const int i = g >> 2, j = g & 3;
+            if (g < 4) a[1][g] = read_frag(cur, a_off, g, 3);
+            else if (g < 8) b[1][g - 4] = read_frag(cur, b_off, g - 4, 3);
+            if (g < 8) {
+                store_chunk<EDGE>(f.a[g], nxt, M, K, m0, (kt + 1) * BK, g);
+                f.a[g] = load_chunk(A, M, K, lda, m0, (kt + 2) * BK, g);
+            } else {
+                store_chunk<EDGE>(f.b[g - 8], nxt + A_STAGE, N, K, n0, (kt + 1) * BK, g - 8);
+                f.b[g - 8] = load_chunk(Bt, N, K, ldb, n0, (kt + 2) * BK, g - 8);
+            }
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // slice 3: half of its MFMAs cover the LDS writes before the barrier,
+        // the other half the reads of the next stage's slice 0 after it
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 8; g < 16; ++g) {
+            if (g < 12) a[0][g - 8] = read_frag(nxt, a_off, g - 8, 0);
+            else b[0][g - 12] = read_frag(nxt, b_off, g - 12, 0);
+            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// Accumulator element r of a 32x32 MFMA tile held by `lane`:
+//   row = (r/4)*8 + (lane/32)*4 + r%4,  col = lane%32.
+__device__ __forceinline__ int acc_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
+
+}  // namespace gemm
+}  // namespace int8k

@@ -109,8 +109,211 @@ torch::Tensor int8_decode_attention_forward_torch(torch::Tensor Q, torch::Tensor
     return out;
 }
 
+// ── INT8 MLP ────────────────────────────────────────────────────────────────
+// Mirrors the four MLP bindings of kernels/int8_ext.cu:188-455.  One C ABI
+// entry point (int8k_mlp_forward) serves all of them through its flags.
+
+namespace {
+
+struct MlpDims {
+    int64_t batch, seq_len, d_model, d_ff, T;
+};
+
+MlpDims check_mlp_args(const torch::Tensor& x, const torch::Tensor& W1, const torch::Tensor& W2,
+                       bool prepacked) {
+    TORCH_CHECK(x.device().is_cuda(), "x must be a CUDA tensor");
+    TORCH_CHECK(x.dtype() == torch::kInt8, "x must be int8");
+    const char* n1 = prepacked ? "W1T" : "W1";
+    const char* n2 = prepacked ? "W2T" : "W2";
+    TORCH_CHECK(W1.dtype() == torch::kInt8, n1, " must be int8");
+    TORCH_CHECK(W2.dtype() == torch::kInt8, n2, " must be int8");
+    TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+    TORCH_CHECK(W1.is_contiguous(), n1, " must be contiguous");
+    TORCH_CHECK(W2.is_contiguous(), n2, " must be contiguous");
+    TORCH_CHECK(x.dim() == 3, "x must be 3-D (batch, seq_len, d_model)");
+    TORCH_CHECK(W1.dim() == 2, prepacked ? "W1T must be 2-D (d_ff, d_model)"
+                                         : "W1 must be 2-D (d_model, d_ff)");
+    TORCH_CHECK(W2.dim() == 2, prepacked ? "W2T must be 2-D (d_model, d_ff)"
+                                         : "W2 must be 2-D (d_ff, d_model)");
+    TORCH_CHECK(W1.device() == x.device() && W2.device() == x.device(),
+                "x/W1/W2 must be on the same device");
+    MlpDims d;
+    d.batch = x.size(0);
+    d.seq_len = x.size(1);
+    d.d_model = x.size(2);
+    d.T = d.batch * d.seq_len;
+    if (prepacked) {
+        d.d_ff = W1.size(0);
+        TORCH_CHECK(W1.size(1) == d.d_model, "W1T shape mismatch (expected d_model cols)");
+        TORCH_CHECK(W2.size(0) == d.d_model, "W2T shape mismatch (expected d_model rows)");
+        TORCH_CHECK(W2.size(1) == d.d_ff, "W2T shape mismatch (expected d_ff cols)");
+    } else {
+        d.d_ff = W1.size(1);
+        TORCH_CHECK(W1.size(0) == d.d_model, "W1 shape mismatch");
+        TORCH_CHECK(W2.size(0) == d.d_ff, "W2 shape mismatch");
+        TORCH_CHECK(W2.size(1) == d.d_model, "W2 shape mismatch");
+    }
+    TORCH_CHECK(d.d_model % 16 == 0 && d.d_ff % 16 == 0,
+                "int8 MLP needs d_model and d_ff to be multiples of 16");
+    TORCH_CHECK(d.T > 0 && d.T <= INT32_MAX && d.d_ff <= INT32_MAX, "MLP shape out of range");
+    return d;
+}
+
+torch::Tensor scalar_scale(double v, const torch::Device& dev) {
+    return torch::full({1}, (float)v, torch::TensorOptions().dtype(torch::kFloat32).device(dev));
+}
+
+void check_scale(const torch::Tensor& s, int64_t n, const char* nm, const torch::Device& dev) {
+    TORCH_CHECK(s.dtype() == torch::kFloat32, nm, " must be float32");
+    TORCH_CHECK(s.device().is_cuda(), nm, " must be CUDA");
+    TORCH_CHECK(s.device() == dev, nm, " must be on x's device");
+    TORCH_CHECK(s.numel() == n || s.numel() == 1, nm, " must have ", n, " (or 1) elements");
+}
+
+// Runs the MLP; returns (out int8 like x, out_scale fp32 [T] or [1]).
+std::tuple<torch::Tensor, torch::Tensor> run_mlp(const torch::Tensor& x, const torch::Tensor& W1,
+                                                 const torch::Tensor& W2, const torch::Tensor& sx,
+                                                 const torch::Tensor& sw1,
+                                                 const torch::Tensor& sw2,
+                                                 const c10::optional<torch::Tensor>& bias1,
+                                                 const MlpDims& d, int flags) {
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+    auto xa = aligned_i8(x), w1 = aligned_i8(W1), w2 = aligned_i8(W2);
+    auto out = torch::empty_like(x);
+    const bool per_tensor = (flags & INT8K_MLP_OUT_PER_TENSOR) != 0;
+    auto out_scale = torch::empty({per_tensor ? 1 : d.T},
+                                  torch::TensorOptions().dtype(torch::kFloat32).device(x.device()));
+    const size_t ws_bytes =
+        int8k_mlp_workspace_bytes((int)d.T, (int)d.d_model, (int)d.d_ff, flags);
+    auto ws = workspace(ws_bytes, x.device());
+    const int st = int8k_mlp_forward(
+        xa.data_ptr<int8_t>(), w1.data_ptr<int8_t>(), w2.data_ptr<int8_t>(),
+        out.data_ptr<int8_t>(), sx.data_ptr<float>(), (int)sx.numel(), sw1.data_ptr<float>(),
+        (int)sw1.numel(), sw2.data_ptr<float>(), (int)sw2.numel(),
+        bias1 ? bias1->data_ptr<float>() : nullptr, out_scale.data_ptr<float>(), (int)d.T,
+        (int)d.d_model, (int)d.d_ff, flags, ws.data_ptr(), ws_bytes, current_stream(x));
+    check_status(st, "int8_mlp_forward");
+    return {out, out_scale};
+}
+
+}  // namespace
+
+// Per-tensor scales (kernels/int8_ext.cu:188-233): returns (int8 out, float out_scale).
+// Reading the scale back is the only host synchronisation.
+std::tuple<torch::Tensor, double> int8_mlp_forward_torch(torch::Tensor x, torch::Tensor W1,
+                                                         torch::Tensor W2, double scale_x,
+                                                         double scale_W1, double scale_W2) {
+    const MlpDims d = check_mlp_args(x, W1, W2, false);
+    auto r = run_mlp(x, W1, W2, scalar_scale(scale_x, x.device()),
+                     scalar_scale(scale_W1, x.device()), scalar_scale(scale_W2, x.device()),
+                     c10::nullopt, d, INT8K_MLP_OUT_PER_TENSOR);
+    return {std::get<0>(r), (double)std::get<1>(r).item<float>()};
+}
+
+// Per-token activation + per-channel weight scales (kernels/int8_ext.cu:246-300):
+// scale_x [T] (or [1]), scale_W1 [d_ff] (or [1]), scale_W2 [d_model] (or [1]);
+// returns (int8 out, fp32 out_scale [T]) — the output is quantized per token.
+std::tuple<torch::Tensor, torch::Tensor> int8_mlp_forward_pc_torch(
+    torch::Tensor x, torch::Tensor W1, torch::Tensor W2, torch::Tensor scale_x,
+    torch::Tensor scale_W1, torch::Tensor scale_W2) {
+    const MlpDims d = check_mlp_args(x, W1, W2, false);
+    check_scale(scale_x, d.T, "scale_x", x.device());
+    check_scale(scale_W1, d.d_ff, "scale_W1", x.device());
+    check_scale(scale_W2, d.d_model, "scale_W2", x.device());
+    return run_mlp(x, W1, W2, scale_x.contiguous(), scale_W1.contiguous(), scale_W2.contiguous(),
+                   c10::nullopt, d, 0);
+}
+
+// As above plus a per-channel pre-GELU bias b1 [d_ff] (kernels/int8_ext.cu:306-365).
+std::tuple<torch::Tensor, torch::Tensor> int8_mlp_forward_pc_bias_torch(
+    torch::Tensor x, torch::Tensor W1, torch::Tensor W2, torch::Tensor scale_x,
+    torch::Tensor scale_W1, torch::Tensor scale_W2, torch::Tensor bias1) {
+    const MlpDims d = check_mlp_args(x, W1, W2, false);
+    check_scale(scale_x, d.T, "scale_x", x.device());
+    check_scale(scale_W1, d.d_ff, "scale_W1", x.device());
+    check_scale(scale_W2, d.d_model, "scale_W2", x.device());
+    TORCH_CHECK(bias1.dtype() == torch::kFloat32, "bias1 must be float32");
+    TORCH_CHECK(bias1.device().is_cuda(), "bias1 must be CUDA");
+    TORCH_CHECK(bias1.device() == x.device(), "bias1 must be on x's device");
+    TORCH_CHECK(bias1.numel() == d.d_ff, "bias1 must have d_ff elements");
+    return run_mlp(x, W1, W2, scale_x.contiguous(), scale_W1.contiguous(), scale_W2.contiguous(),
+                   bias1.contiguous(), d, 0);
+}
+
+// W1 (d_model, d_ff) -> W1T (d_ff, d_model); W2 (d_ff, d_model) -> W2T (d_model, d_ff)
+// (kernels/int8_ext.cu:372-399).
+std::tuple<torch::Tensor, torch::Tensor> transpose_int8_weights_torch(torch::Tensor W1,
+                                                                      torch::Tensor W2) {
+    TORCH_CHECK(W1.device().is_cuda(), "W1 must be a CUDA tensor");
+    TORCH_CHECK(W1.dtype() == torch::kInt8, "W1 must be int8");
+    TORCH_CHECK(W2.dtype() == torch::kInt8, "W2 must be int8");
+    TORCH_CHECK(W1.is_contiguous(), "W1 must be contiguous");
+    TORCH_CHECK(W2.is_contiguous(), "W2 must be contiguous");
+    TORCH_CHECK(W1.dim() == 2, "W1 must be 2-D (d_model, d_ff)");
+    TORCH_CHECK(W2.dim() == 2, "W2 must be 2-D (d_ff, d_model)");
+    const int64_t d_model = W1.size(0), d_ff = W1.size(1);
+    TORCH_CHECK(W2.size(0) == d_ff, "W2 shape mismatch (expected d_ff rows)");
+    TORCH_CHECK(W2.size(1) == d_model, "W2 shape mismatch (expected d_model cols)");
+    TORCH_CHECK(W2.device() == W1.device(), "W1/W2 must be on the same device");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(W1.device());
+    auto opts = torch::TensorOptions().dtype(torch::kInt8).device(W1.device());
+    auto W1T = torch::empty({d_ff, d_model}, opts);
+    auto W2T = torch::empty({d_model, d_ff}, opts);
+    const int st = int8k_transpose_int8_weights(W1.data_ptr<int8_t>(), W2.data_ptr<int8_t>(),
+                                                W1T.data_ptr<int8_t>(), W2T.data_ptr<int8_t>(),
+                                                (int)d_model, (int)d_ff, current_stream(W1));
+    check_status(st, "transpose_int8_weights");
+    return {W1T, W2T};
+}
+
+// Per-tensor MLP on pre-transposed weights (kernels/int8_ext.cu:407-455).  The
+// reference also demands T, d_model, d_ff % 128 == 0 (its WMMA tiles); these
+// kernels handle any T and need only d_model, d_ff % 16 == 0.
+std::tuple<torch::Tensor, double> int8_mlp_forward_prepacked_torch(torch::Tensor x,
+                                                                   torch::Tensor W1T,
+                                                                   torch::Tensor W2T,
+                                                                   double scale_x,
+                                                                   double scale_W1,
+                                                                   double scale_W2) {
+    const MlpDims d = check_mlp_args(x, W1T, W2T, true);
+    auto r = run_mlp(x, W1T, W2T, scalar_scale(scale_x, x.device()),
+                     scalar_scale(scale_W1, x.device()), scalar_scale(scale_W2, x.device()),
+                     c10::nullopt, d, INT8K_MLP_WEIGHTS_PREPACKED | INT8K_MLP_OUT_PER_TENSOR);
+    return {std::get<0>(r), (double)std::get<1>(r).item<float>()};
+}
+
+// New overload (not in the reference): per-token / per-channel scales on
+// pre-transposed weights, for static-weight inference on the per-channel path.
+// Same results as int8_mlp_forward's tensor overload on the untransposed weights.
+std::tuple<torch::Tensor, torch::Tensor> int8_mlp_forward_prepacked_pc_torch(
+    torch::Tensor x, torch::Tensor W1T, torch::Tensor W2T, torch::Tensor scale_x,
+    torch::Tensor scale_W1, torch::Tensor scale_W2) {
+    const MlpDims d = check_mlp_args(x, W1T, W2T, true);
+    check_scale(scale_x, d.T, "scale_x", x.device());
+    check_scale(scale_W1, d.d_ff, "scale_W1", x.device());
+    check_scale(scale_W2, d.d_model, "scale_W2", x.device());
+    return run_mlp(x, W1T, W2T, scale_x.contiguous(), scale_W1.contiguous(),
+                   scale_W2.contiguous(), c10::nullopt, d, INT8K_MLP_WEIGHTS_PREPACKED);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("int8_decode_attention_forward", &int8_decode_attention_forward_torch,
           "INT8 flash-decoding attention (seq_q==1, INT8 KV cache) — returns FP16");
+    // Two overloads: scalar scales (per-tensor) and tensor scales (per-token
+    // activation + per-channel weight); pybind11 dispatches by argument type.
+    m.def("int8_mlp_forward", &int8_mlp_forward_torch,
+          "INT8 MLP, per-tensor scales — returns (int8_out, out_scale)");
+    m.def("int8_mlp_forward", &int8_mlp_forward_pc_torch,
+          "INT8 MLP, per-token/per-channel scales — returns (int8_out, out_scale[T])");
+    m.def("int8_mlp_forward_per_channel_bias", &int8_mlp_forward_pc_bias_torch,
+          "INT8 MLP, per-token/per-channel scales + per-channel pre-GELU bias b1 — "
+          "returns (int8_out, out_scale[T])");
+    m.def("transpose_int8_weights", &transpose_int8_weights_torch,
+          "Pre-transpose INT8 W1/W2 to [N][K] for the prepacked MLP path — returns (W1T, W2T)");
+    m.def("int8_mlp_forward_prepacked", &int8_mlp_forward_prepacked_torch,
+          "INT8 MLP, per-tensor scales, pre-transposed weights — returns (int8_out, out_scale)");
+    m.def("int8_mlp_forward_prepacked", &int8_mlp_forward_prepacked_pc_torch,
+          "INT8 MLP, per-token/per-channel scales, pre-transposed weights — "
+          "returns (int8_out, out_scale[T])");
     m.attr("abi_version") = int8k_abi_version();
 }

@@ -63,6 +63,11 @@ __device__ __forceinline__ int dpp_half_mirror(int v) {
     return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
 }
 
+// row_mirror: lane i of each 16-lane row reads lane 15-i.
+__device__ __forceinline__ int dpp_row_mirror(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+}
+
 // Sum over each aligned group of 4 lanes; every lane of the group gets it.
 __device__ __forceinline__ int group4_sum(int v) {
     v += dpp_xor1(v);

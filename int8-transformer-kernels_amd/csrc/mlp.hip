@@ -1,0 +1,421 @@
+// mlp.hip — INT8 two-GEMM MLP with dynamic per-token requantization (gfx950).
+//
+// Contract of the reference's int8_mlp_forward_impl dynamic path
+// (kernels/int8_mlp.cu:999-1191) and its public launchers
+// int8_mlp_forward / _per_channel / _per_channel_bias / _prepacked and
+// transpose_int8_weights (kernels/int8_mlp.cu:1231-1314):
+//
+//   GEMM1   acc1 = x . W1                       (s8 x s8 -> exact s32)
+//   epi1    v = (f32(acc1) * sx[t]) * sW1[n] (+ b1[n]);  v = GELU_tanh(v)
+//           hidden = fp16(v);  rowmax_t = max_n |v|  (fp32, before rounding)
+//   requant hq = rn(clamp(f32(hidden) * 127/max(rowmax,1e-8)));  sh[t] = max(rowmax,1e-8)/127
+//   GEMM2   acc2 = hq . W2
+//   epi2    o = (f32(acc2) * sh[t]) * sW2[n];  out16 = fp16(o);  rowmax / tensor max of |o|
+//   quant   out = rn(clamp(f32(out16) * 127/amax)),  out_scale = amax/127 (per token or tensor)
+//
+// Kernels: gemm_i8_kernel<EPI> (the MFMA core of gemm_i8.h with a fused
+// epilogue: scales, bias, GELU, fp16 store and per-(tile, row) absmax partials
+// — no atomics, no zero-fill), requant_rows_kernel (reduces the partials,
+// requantizes a row), tensor_absmax_kernel and transpose_i8_kernel (weight
+// packing to the K-contiguous [N][K] layout the MFMA operands want).
+#include <algorithm>
+
+#include "gemm_i8.h"
+
+namespace int8k {
+namespace {
+
+using namespace gemm;
+
+enum EpiMode { EPI_I32 = 0, EPI_GELU_F16 = 1, EPI_F16 = 2 };
+
+struct EpiParams {
+    int32_t* c32;        // EPI_I32 output
+    uint16_t* c16;       // fp16 output
+    int ldc;
+    const float* sa;     // per-row scale (stride sa_stride: 0 = scalar)
+    int sa_stride;
+    const float* sb;     // per-column scale
+    int sb_stride;
+    const float* bias;   // per-column bias or null
+    float* pmax;         // [tiles_n][M] row absmax partials
+};
+
+// GELU, tanh form: 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi)(x + 0.044715 x^3).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return x * __builtin_amdgcn_rcpf(1.f + fast_exp2(-2.f * kLog2e * u));
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int M, int N, int K, int lda,
+    int ldb, int tiles_m, int tiles_n, EpiParams p) {
+    extern __shared__ __align__(16) char lds[];
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    v16i acc[TM][TN];
+    // interior tiles take the unmasked operand path
+    if (m0 + BM <= M && n0 + BN <= N && K % BK == 0)
+        mainloop<false>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
+    else
+        mainloop<true>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int rbase = m0 + wm * WM;
+    const int cbase = n0 + wn * WN + (lane & 31);
+
+    if constexpr (EPI == EPI_I32) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = cbase + j * 32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + i * 32 + acc_row(r, lane);
+                    if (row < M && col < N) p.c32[(size_t)row * p.ldc + col] = acc[i][j][r];
+                }
+            }
+        return;
+    } else {
+        // Row absmax of this block's tile, gathered in LDS (values >= 0, so
+        // integer max on the bit pattern orders them like floats).
+        int* rowmax = reinterpret_cast<int*>(lds);
+        for (int i = threadIdx.x; i < BM; i += kThreads) rowmax[i] = 0;
+        __syncthreads();
+        const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
+        const bool odd = lane & 1;
+        float sbv[TN], biv[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = cbase + j * 32;
+            sbv[j] = col < N ? p.sb[(size_t)col * p.sb_stride] : 0.f;
+            biv[j] = (p.bias != nullptr && col < N) ? p.bias[col] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float sav[16], rmax[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + i * 32 + acc_row(r, lane);
+                sav[r] = row < M ? p.sa[(size_t)row * p.sa_stride] : 0.f;
+                rmax[r] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = cbase + j * 32;
+                const bool cok = col < N;
+                float v[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    v[r] = static_cast<float>(acc[i][j][r]) * sav[r] * sbv[j];
+                    if constexpr (EPI == EPI_GELU_F16) v[r] = gelu_tanh(v[r] + biv[j]);
+                    if (cok) rmax[r] = fmaxf(rmax[r], fabsf(v[r]));
+                }
+                if (interior) {
+                    // Rows r, r+1 are consecutive; lanes 2k, 2k+1 hold columns c, c+1.
+                    // Exchange one half so the even lane stores (r, c..c+1) and the
+                    // odd lane (r+1, c..c+1) as one 32-bit word each.
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        const uint32_t h0 = f32_to_f16_bits(v[r]);
+                        const uint32_t h1 = f32_to_f16_bits(v[r + 1]);
+                        const uint32_t recv = (uint32_t)dpp_xor1((int)(odd ? h0 : h1));
+                        const uint32_t word = odd ? (recv | (h1 << 16)) : (h0 | (recv << 16));
+                        const int row = rbase + i * 32 + acc_row(r, lane) + (odd ? 1 : 0);
+                        *reinterpret_cast<uint32_t*>(p.c16 + (size_t)row * p.ldc + (col & ~1)) =
+                            word;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = rbase + i * 32 + acc_row(r, lane);
+                        if (row < M && cok)
+                            p.c16[(size_t)row * p.ldc + col] = f32_to_f16_bits(v[r]);
+                    }
+                }
+            }
+            // Max over the 32 lanes that share these rows: DPP inside each
+            // 16-lane row, then one swizzle across the two rows of the half.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int m = __float_as_int(rmax[r]);
+                m = max(m, dpp_xor1(m));
+                m = max(m, dpp_xor2(m));
+                m = max(m, dpp_half_mirror(m));
+                m = max(m, dpp_row_mirror(m));
+                m = max(m, __builtin_amdgcn_ds_swizzle(m, 0x401f));
+                if ((lane & 31) == 0) atomicMax(&rowmax[wm * WM + i * 32 + acc_row(r, lane)], m);
+            }
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < BM; i += kThreads) {
+            const int row = m0 + i;
+            if (row < M) p.pmax[(size_t)tn * M + row] = __int_as_float(rowmax[i]);
+        }
+    }
+}
+
+// One block per row: reduce the row's absmax partials, then requantize the
+// fp16 row to int8 with scale max(amax,1e-8)/127 (quantize_rows semantics).
+// With `tensor_amax` set, that single value is used for every row instead
+// and `scales` receives it once (per-tensor output quantization).
+__global__ __launch_bounds__(256) void requant_rows_kernel(
+    const uint16_t* __restrict__ h, int ldh, const float* __restrict__ pmax, int tiles_n,
+    const float* __restrict__ tensor_amax, int8_t* __restrict__ q, int ldq,
+    float* __restrict__ scales, int M, int N) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    float amax;
+    if (tensor_amax != nullptr) {
+        amax = *tensor_amax;
+    } else {
+        float m = 0.f;
+        for (int t = threadIdx.x; t < tiles_n; t += 256) m = fmaxf(m, pmax[(size_t)t * M + row]);
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+        __syncthreads();
+        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    }
+    amax = fmaxf(amax, 1e-8f);
+    const float inv = 127.f / amax;
+    if (threadIdx.x == 0 && (tensor_amax == nullptr || row == 0))
+        scales[tensor_amax == nullptr ? row : 0] = amax / 127.f;
+    const uint16_t* hr = h + (size_t)row * ldh;
+    int8_t* qr = q + (size_t)row * ldq;
+    auto quant = [inv](uint16_t bits) -> int {
+        const float f = __half2float(__ushort_as_half(bits)) * inv;
+        return static_cast<int>(__builtin_rintf(fminf(fmaxf(f, -128.f), 127.f)));
+    };
+    if ((N & 7) == 0 && (ldh & 7) == 0 && (ldq & 7) == 0) {
+        for (int c = threadIdx.x * 8; c < N; c += 256 * 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(hr + c);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                lo |= (uint32_t)(quant(w[e] & 0xffff) & 0xff) << (16 * e);
+                lo |= (uint32_t)(quant(w[e] >> 16) & 0xff) << (16 * e + 8);
+                hi |= (uint32_t)(quant(w[2 + e] & 0xffff) & 0xff) << (16 * e);
+                hi |= (uint32_t)(quant(w[2 + e] >> 16) & 0xff) << (16 * e + 8);
+            }
+            *reinterpret_cast<uint2*>(qr + c) = make_uint2(lo, hi);
+        }
+    } else {
+        for (int c = threadIdx.x; c < N; c += 256) qr[c] = (int8_t)quant(hr[c]);
+    }
+}
+
+// Max over all partials (per-tensor output scale), one block.
+__global__ __launch_bounds__(256) void tensor_absmax_kernel(const float* __restrict__ pmax,
+                                                            size_t n, float* __restrict__ out) {
+    __shared__ float red[4];
+    float m = 0.f;
+    for (size_t i = threadIdx.x; i < n; i += 256) m = fmaxf(m, pmax[i]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) *out = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// dst[C][R] = src[R][C]^T through a 64x64 LDS tile.
+__global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ src,
+                                                           int8_t* __restrict__ dst, int R, int C) {
+    __shared__ int8_t tile[64][65];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i / 64, c = i % 64;
+        if (r0 + r < R && c0 + c < C) tile[r][c] = src[(size_t)(r0 + r) * C + c0 + c];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int c = i / 64, r = i % 64;
+        if (r0 + r < R && c0 + c < C) dst[(size_t)(c0 + c) * R + r0 + r] = tile[r][c];
+    }
+}
+
+template <int EPI>
+int launch_gemm(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
+                hipStream_t stream) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    gemm_i8_kernel<EPI><<<tiles_m * tiles_n, kThreads, LDS_BYTES, stream>>>(
+        A, Bt, M, N, K, K, K, tiles_m, tiles_n, p);
+    return check_launch("gemm_i8_kernel");
+}
+
+int launch_transpose(const int8_t* src, int8_t* dst, int R, int C, hipStream_t stream) {
+    const dim3 grid((C + 63) / 64, (R + 63) / 64);
+    transpose_i8_kernel<<<grid, 256, 0, stream>>>(src, dst, R, C);
+    return check_launch("transpose_i8_kernel");
+}
+
+// Workspace layout of one MLP call (all offsets 256-byte aligned).
+struct MlpWorkspace {
+    int8_t* w1t;      // [d_ff][d_model]  (absent when prepacked)
+    int8_t* w2t;      // [d_model][d_ff]
+    uint16_t* h16;    // [T][d_ff]
+    int8_t* hq;       // [T][d_ff]
+    float* sh;        // [T]
+    float* p1;        // [tiles_n1][T]
+    uint16_t* o16;    // [T][d_model]
+    float* p2;        // [tiles_n2][T]
+    float* tmax;      // [1]
+    size_t bytes;
+};
+
+MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
+    char* p = static_cast<char*>(base);
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        char* r = p + off;
+        off += round_up(n, kWorkspaceAlign);
+        return r;
+    };
+    MlpWorkspace w{};
+    const size_t wbytes = prepacked ? 0 : (size_t)dm * dff;
+    w.w1t = reinterpret_cast<int8_t*>(take(wbytes));
+    w.w2t = reinterpret_cast<int8_t*>(take(wbytes));
+    w.h16 = reinterpret_cast<uint16_t*>(take((size_t)T * dff * 2));
+    w.hq = reinterpret_cast<int8_t*>(take((size_t)T * dff));
+    w.sh = reinterpret_cast<float*>(take((size_t)T * 4));
+    w.p1 = reinterpret_cast<float*>(take((size_t)((dff + BN - 1) / BN) * T * 4));
+    w.o16 = reinterpret_cast<uint16_t*>(take((size_t)T * dm * 2));
+    w.p2 = reinterpret_cast<float*>(take((size_t)((dm + BN - 1) / BN) * T * 4));
+    w.tmax = reinterpret_cast<float*>(take(4));
+    w.bytes = off;
+    return w;
+}
+
+bool lds_configured = false;
+
+int configure_lds() {
+    if (lds_configured) return INT8K_OK;
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_I32>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_GELU_F16>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (e != hipSuccess) {
+        set_last_error("hipFuncSetAttribute", e);
+        return INT8K_ERR_HIP;
+    }
+    lds_configured = true;
+    return INT8K_OK;
+}
+
+}  // namespace
+}  // namespace int8k
+
+using namespace int8k;
+
+extern "C" int int8k_gemm_i8_i32(const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N,
+                                 int K, void* stream) {
+    clear_last_error();
+    if (!A || !Bt || !C || M <= 0 || N <= 0 || K <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (K % 16 != 0) return INT8K_ERR_UNSUPPORTED;
+    if (!aligned_to(A, 16) || !aligned_to(Bt, 16) || !aligned_to(C, 4)) return INT8K_ERR_MISALIGNED;
+    int st = configure_lds();
+    if (st != INT8K_OK) return st;
+    EpiParams p{};
+    p.c32 = C;
+    p.ldc = N;
+    return launch_gemm<EPI_I32>(A, Bt, M, N, K, p, as_stream(stream));
+}
+
+extern "C" int int8k_transpose_int8_weights(const int8_t* W1, const int8_t* W2, int8_t* W1T,
+                                            int8_t* W2T, int d_model, int d_ff, void* stream) {
+    clear_last_error();
+    if (!W1 || !W2 || !W1T || !W2T || d_model <= 0 || d_ff <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    int st = launch_transpose(W1, W1T, d_model, d_ff, as_stream(stream));
+    if (st != INT8K_OK) return st;
+    return launch_transpose(W2, W2T, d_ff, d_model, as_stream(stream));
+}
+
+extern "C" size_t int8k_mlp_workspace_bytes(int T, int d_model, int d_ff, int flags) {
+    if (T <= 0 || d_model <= 0 || d_ff <= 0) return 0;
+    return carve_mlp(nullptr, T, d_model, d_ff, (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0).bytes;
+}
+
+extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t* W2, int8_t* out,
+                                 const float* scale_x, int n_scale_x, const float* scale_W1,
+                                 int n_scale_W1, const float* scale_W2, int n_scale_W2,
+                                 const float* bias1, float* out_scale, int T, int d_model,
+                                 int d_ff, int flags, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+    clear_last_error();
+    if (!x || !W1 || !W2 || !out || !scale_x || !scale_W1 || !scale_W2 || !out_scale)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (T <= 0 || d_model <= 0 || d_ff <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if ((n_scale_x != 1 && n_scale_x != T) || (n_scale_W1 != 1 && n_scale_W1 != d_ff) ||
+        (n_scale_W2 != 1 && n_scale_W2 != d_model))
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if ((flags & ~(INT8K_MLP_WEIGHTS_PREPACKED | INT8K_MLP_OUT_PER_TENSOR)) != 0)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (d_model % 16 != 0 || d_ff % 16 != 0) return INT8K_ERR_UNSUPPORTED;
+    if (!aligned_to(x, 16) || !aligned_to(W1, 16) || !aligned_to(W2, 16) || !aligned_to(out, 4) ||
+        !aligned_to(scale_x, 4) || !aligned_to(scale_W1, 4) || !aligned_to(scale_W2, 4) ||
+        !aligned_to(out_scale, 4) || (bias1 && !aligned_to(bias1, 4)))
+        return INT8K_ERR_MISALIGNED;
+    const bool prepacked = (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0;
+    const bool per_tensor_out = (flags & INT8K_MLP_OUT_PER_TENSOR) != 0;
+    const MlpWorkspace w = carve_mlp(workspace, T, d_model, d_ff, prepacked);
+    if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
+    if (!aligned_to(workspace, 256)) return INT8K_ERR_MISALIGNED;
+    int st = configure_lds();
+    if (st != INT8K_OK) return st;
+    hipStream_t s = as_stream(stream);
+
+    const int8_t* W1t = W1;
+    const int8_t* W2t = W2;
+    if (!prepacked) {
+        if ((st = launch_transpose(W1, w.w1t, d_model, d_ff, s)) != INT8K_OK) return st;
+        if ((st = launch_transpose(W2, w.w2t, d_ff, d_model, s)) != INT8K_OK) return st;
+        W1t = w.w1t;
+        W2t = w.w2t;
+    }
+    // GEMM1 + scale/bias/GELU epilogue -> fp16 hidden + row absmax partials
+    EpiParams p1{};
+    p1.c16 = w.h16;
+    p1.ldc = d_ff;
+    p1.sa = scale_x;
+    p1.sa_stride = n_scale_x == 1 ? 0 : 1;
+    p1.sb = scale_W1;
+    p1.sb_stride = n_scale_W1 == 1 ? 0 : 1;
+    p1.bias = bias1;
+    p1.pmax = w.p1;
+    if ((st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s)) != INT8K_OK) return st;
+    // per-token requant of the hidden
+    const int tn1 = (d_ff + BN - 1) / BN;
+    requant_rows_kernel<<<T, 256, 0, s>>>(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T,
+                                          d_ff);
+    if ((st = check_launch("requant_rows_kernel")) != INT8K_OK) return st;
+    // GEMM2 + dequant epilogue -> fp16 output + absmax partials
+    EpiParams p2{};
+    p2.c16 = w.o16;
+    p2.ldc = d_model;
+    p2.sa = w.sh;
+    p2.sa_stride = 1;
+    p2.sb = scale_W2;
+    p2.sb_stride = n_scale_W2 == 1 ? 0 : 1;
+    p2.pmax = w.p2;
+    if ((st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s)) != INT8K_OK) return st;
+    const int tn2 = (d_model + BN - 1) / BN;
+    const float* tmax = nullptr;
+    if (per_tensor_out) {
+        tensor_absmax_kernel<<<1, 256, 0, s>>>(w.p2, (size_t)tn2 * T, w.tmax);
+        if ((st = check_launch("tensor_absmax_kernel")) != INT8K_OK) return st;
+        tmax = w.tmax;
+    }
+    requant_rows_kernel<<<T, 256, 0, s>>>(w.o16, d_model, w.p2, tn2, tmax, out, d_model,
+                                          out_scale, T, d_model);
+    return check_launch("requant_rows_kernel");
+}

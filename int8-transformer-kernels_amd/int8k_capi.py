@@ -38,7 +38,15 @@ _SIGNATURES = {
     "int8k_decode_attention_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "int8k_decode_attention_num_splits": (_I, [_I, _I, _I, _I]),
     "int8k_decode_attention_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
+    "int8k_mlp_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "int8k_mlp_forward": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _P, _P, _I, _I, _I, _I,
+                               _P, _SZ, _P]),
+    "int8k_transpose_int8_weights": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "int8k_gemm_i8_i32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
 }
+
+MLP_WEIGHTS_PREPACKED = 1
+MLP_OUT_PER_TENSOR = 2
 
 _lib = None
 
@@ -119,3 +127,63 @@ def decode_attention(Qi, Ki, Vi, sQ, sK, sV, nsplit: int = 0, out=None, workspac
         BH, S, D, nsplit, _ptr(workspace), workspace.numel(), _stream(Qi))
     check("int8k_decode_attention_forward", st)
     return out
+
+
+# --------------------------------------------------------------------------
+# MLP / GEMM
+# --------------------------------------------------------------------------
+
+
+def gemm_i8_i32(A, Bt, out=None):
+    """C[M,N] = A[M,K] . Bt[N,K]^T, exact int32 (device tensors)."""
+    import torch
+
+    M, K = A.shape
+    N = Bt.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32, device=A.device)
+    check("int8k_gemm_i8_i32",
+          load().int8k_gemm_i8_i32(_ptr(A), _ptr(Bt), _ptr(out), M, N, K, _stream(A)))
+    return out
+
+
+def transpose_int8_weights(W1, W2):
+    import torch
+
+    dm, dff = W1.shape
+    W1T = torch.empty((dff, dm), dtype=torch.int8, device=W1.device)
+    W2T = torch.empty((dm, dff), dtype=torch.int8, device=W1.device)
+    check("int8k_transpose_int8_weights",
+          load().int8k_transpose_int8_weights(_ptr(W1), _ptr(W2), _ptr(W1T), _ptr(W2T), dm, dff,
+                                              _stream(W1)))
+    return W1T, W2T
+
+
+def mlp_workspace_bytes(T, d_model, d_ff, flags=0):
+    return load().int8k_mlp_workspace_bytes(T, d_model, d_ff, flags)
+
+
+def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, flags=0, out=None, out_scale=None,
+                workspace=None):
+    """x [T, d_model] int8; W1/W2 int8 ([K][N], or [N][K] with MLP_WEIGHTS_PREPACKED);
+    scales fp32 device tensors of length 1 or full.  Returns (out int8, out_scale fp32)."""
+    import torch
+
+    dm = x.shape[-1]
+    T = x.numel() // dm
+    prepacked = bool(flags & MLP_WEIGHTS_PREPACKED)
+    dff = W1.shape[0] if prepacked else W1.shape[1]
+    if out is None:
+        out = torch.empty((T, dm), dtype=torch.int8, device=x.device)
+    if out_scale is None:
+        n = 1 if flags & MLP_OUT_PER_TENSOR else T
+        out_scale = torch.empty(n, dtype=torch.float32, device=x.device)
+    ws_bytes = mlp_workspace_bytes(T, dm, dff, flags)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    st = load().int8k_mlp_forward(
+        _ptr(x), _ptr(W1), _ptr(W2), _ptr(out), _ptr(sx), sx.numel(), _ptr(sW1), sW1.numel(),
+        _ptr(sW2), sW2.numel(), _ptr(bias1), _ptr(out_scale), T, dm, dff, flags,
+        _ptr(workspace), workspace.numel(), _stream(x))
+    check("int8k_mlp_forward", st)
+    return out, out_scale

@@ -194,7 +194,8 @@ def _as_scale(s, n):
     return s
 
 
-def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, per_token_out=True, return_stages=False):
+def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, per_token_out=True, return_stages=False,
+                gemm=None):
     """Two-GEMM int8 MLP with dynamic per-token hidden requant.
 
     Reference: int8_mlp_forward_impl dynamic path (kernels/int8_mlp.cu:999-1191):
@@ -207,8 +208,10 @@ def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, per_token_out=True, return_
     x [T, dm] int8; W1 [dm, dff] int8; W2 [dff, dm] int8; sx [T] or [1];
     sW1 [dff] or [1]; sW2 [dm] or [1]; bias1 [dff] or None.
     Returns (out int8 [T, dm], out_scale [T] or scalar) and, when asked, the
-    intermediate stages.
+    intermediate stages.  `gemm` may supply another exact int8 GEMM (the C
+    restatement) for speed.
     """
+    gemm = gemm or gemm_i8_i32
     x = np.asarray(x, np.int8)
     T, dm = x.shape
     dff = np.asarray(W1).shape[1]
@@ -216,7 +219,7 @@ def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, per_token_out=True, return_
     s1 = _as_scale(sW1, dff)
     s2 = _as_scale(sW2, dm)
 
-    acc1 = gemm_i8_i32(x, W1)
+    acc1 = gemm(x, W1)
     v = (acc1.astype(F32) * sxv[:, None]).astype(F32) * s1[None, :]
     v = v.astype(F32)
     if bias1 is not None:
@@ -226,7 +229,7 @@ def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, per_token_out=True, return_
     h_amax = np.abs(v).max(axis=1).astype(F32) if dff else np.zeros(T, F32)
     hq, sh = requant_rows_f16(h16, h_amax)
 
-    acc2 = gemm_i8_i32(hq, W2)
+    acc2 = gemm(hq, W2)
     o = ((acc2.astype(F32) * sh[:, None]).astype(F32) * s2[None, :]).astype(F32)
     o16 = o.astype(F16)
     if per_token_out:

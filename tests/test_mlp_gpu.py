@@ -1,0 +1,182 @@
+"""Parity of the INT8 MLP (and its raw GEMM core) against the CPU oracle (GPU tests).
+
+Bar: int32 accumulators bit-exact; int8 outputs within +-1 LSB of the oracle
+(the oracle keeps the reference's fp32 epilogue order — kernels/int8_mlp.cu:441-449,
+768-795 — so only transcendental/FMA rounding can differ); output scales to
+fp32 rounding.  Shapes cover the reference's per-tensor MLP check
+(tests/test_int8.py:130-154: 2x512, 512 -> 2048), ragged tiles, bias, the
+prepacked path and the BASELINE config 4 at full size (sampled rows — each
+output row depends only on its own input row).
+"""
+import numpy as np
+import pytest
+import torch
+
+import int8k_capi as capi
+import workloads
+from oracle import int8_oracle as O
+from oracle import oracle_c
+
+pytestmark = pytest.mark.gpu
+
+# Largest tolerated share of +-1 LSB disagreements between kernel and oracle.
+MAX_FLIP_FRACTION = 0.02
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (512, 768, 256), (300, 200, 64),
+                                   (1, 16, 16), (257, 513, 4112), (1000, 256, 128)])
+def test_gemm_i32_bit_exact(gpu, M, N, K):
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    A = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    Bt = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    C = capi.gemm_i8_i32(A.to(gpu), Bt.to(gpu))
+    torch.cuda.synchronize()
+    ref = oracle_c.gemm_i8_i32(A.numpy(), Bt.numpy().T.copy())
+    np.testing.assert_array_equal(_np(C), ref)
+
+
+def test_gemm_i32_extreme_values(gpu):
+    # |acc| = 16384 * 128 * 128 = 2^28: the deepest MLP reduction, all -128 codes
+    M, N, K = 256, 256, 16384
+    A = torch.full((M, K), -128, dtype=torch.int8, device=gpu)
+    Bt = torch.full((N, K), -128, dtype=torch.int8, device=gpu)
+    C = capi.gemm_i8_i32(A, Bt)
+    torch.cuda.synchronize()
+    assert int(C.min()) == int(C.max()) == K * 128 * 128
+
+
+def _compare_mlp(out, out_scale, ref_out, ref_scale, label):
+    out = np.asarray(out, np.int32)
+    ref_out = np.asarray(ref_out, np.int32)
+    diff = np.abs(out - ref_out)
+    assert diff.max() <= 1, f"{label}: int8 output off by {diff.max()} LSB"
+    flips = float((diff != 0).mean())
+    assert flips <= MAX_FLIP_FRACTION, f"{label}: {flips:.4f} of codes differ by 1 LSB"
+    np.testing.assert_allclose(np.asarray(out_scale, np.float64),
+                               np.asarray(ref_scale, np.float64), rtol=2e-3)
+    return flips
+
+
+def _mlp_case(T, dm, dff, seed, gpu):
+    c = workloads.mlp_case(T, dm, dff, seed=seed, device=gpu, gen_device="cpu")
+    return c, {k: _np(v) for k, v in c.items()}
+
+
+@pytest.mark.parametrize("T,dm,dff", [(1024, 512, 2048), (256, 1024, 4096), (100, 256, 768),
+                                      (1, 64, 128), (300, 512, 1040)])
+def test_mlp_per_channel_vs_oracle(capi_mlp, gpu, T, dm, dff):
+    c, n = _mlp_case(T, dm, dff, seed=T + dm + dff, gpu=gpu)
+    out, osc = capi.mlp_forward(c["x"].reshape(T, dm), c["W1"], c["W2"], c["sx"], c["sW1"],
+                                c["sW2"])
+    torch.cuda.synchronize()
+    ref, rsc = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                             n["sW2"], gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out), _np(osc), ref, rsc, f"T{T} dm{dm} dff{dff}")
+
+
+def test_mlp_bias_vs_oracle(ext, gpu):
+    T, dm, dff = 384, 512, 2048
+    c, n = _mlp_case(T, dm, dff, seed=42, gpu=gpu)
+    bias = torch.randn(dff, generator=torch.Generator().manual_seed(1)) * 0.5
+    out, osc = ext.int8_mlp_forward_per_channel_bias(c["x"], c["W1"], c["W2"], c["sx"],
+                                                     c["sW1"], c["sW2"], bias.to(gpu))
+    torch.cuda.synchronize()
+    ref, rsc = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                             n["sW2"], bias1=bias.numpy(), gemm=oracle_c.gemm_i8_i32)
+    assert tuple(out.shape) == (1, T, dm) and out.dtype == torch.int8
+    _compare_mlp(_np(out).reshape(T, dm), _np(osc), ref, rsc, "bias")
+
+
+def test_mlp_per_tensor_reference_config(ext, gpu):
+    # tests/test_int8.py:130-154: batch 2, seq 512, 512 -> 2048, per-tensor scales
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(2, 512, 512, generator=g)
+    W1 = torch.randn(512, 2048, generator=g) * 0.02
+    W2 = torch.randn(2048, 512, generator=g) * 0.02
+    xi, sx = O.quantize_per_tensor(x.numpy())
+    w1i, s1 = O.quantize_per_tensor(W1.numpy())
+    w2i, s2 = O.quantize_per_tensor(W2.numpy())
+    out, osc = ext.int8_mlp_forward(torch.from_numpy(xi).to(gpu), torch.from_numpy(w1i).to(gpu),
+                                    torch.from_numpy(w2i).to(gpu), float(sx), float(s1),
+                                    float(s2))
+    assert isinstance(osc, float) and tuple(out.shape) == (2, 512, 512)
+    ref, rsc = O.mlp_forward(xi.reshape(1024, 512), w1i, w2i, sx, s1, s2, per_token_out=False,
+                             gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out).reshape(1024, 512), osc, ref, rsc, "per-tensor")
+    # and the dequantized result tracks the float MLP (common/baseline.py:25-37)
+    deq = _np(out).reshape(1024, 512).astype(np.float64) * osc
+    fref = O.mlp_dequant_reference(xi.reshape(1024, 512), w1i, w2i, sx, s1, s2)
+    assert np.abs(deq - fref).max() < 0.1  # the reference's int8 atol (common/correctness.py:23)
+
+
+def test_mlp_prepacked_matches_unpacked(ext, gpu):
+    T, dm, dff = 512, 512, 2048
+    c, _ = _mlp_case(T, dm, dff, seed=5, gpu=gpu)
+    W1T, W2T = ext.transpose_int8_weights(c["W1"], c["W2"])
+    assert torch.equal(W1T, c["W1"].t().contiguous()) and torch.equal(W2T, c["W2"].t().contiguous())
+    a, sa = ext.int8_mlp_forward(c["x"], c["W1"], c["W2"], c["sx"], c["sW1"], c["sW2"])
+    b, sb = ext.int8_mlp_forward_prepacked(c["x"], W1T, W2T, c["sx"], c["sW1"], c["sW2"])
+    assert torch.equal(a, b) and torch.equal(sa, sb)
+    s = [float(v) for v in (0.01, 0.002, 0.003)]
+    a, sa = ext.int8_mlp_forward(c["x"], c["W1"], c["W2"], *s)
+    b, sb = ext.int8_mlp_forward_prepacked(c["x"], W1T, W2T, *s)
+    assert torch.equal(a, b) and sa == sb
+
+
+def test_mlp_kats_zero_and_constant(ext, gpu):
+    T, dm, dff = 256, 256, 512
+    z = torch.zeros(1, T, dm, dtype=torch.int8, device=gpu)
+    w1 = torch.zeros(dm, dff, dtype=torch.int8, device=gpu)
+    w2 = torch.zeros(dff, dm, dtype=torch.int8, device=gpu)
+    one = lambda n: torch.full((n,), 1e-8 / 127, device=gpu)  # noqa: E731
+    out, osc = ext.int8_mlp_forward(z, w1, w2, one(T), one(dff), one(dm))
+    assert int(out.abs().max()) == 0 and torch.isfinite(osc).all()
+    # constant dataset: every code of the output is 127
+    x = torch.full((1, T, dm), 127, dtype=torch.int8, device=gpu)
+    w1 = torch.full((dm, dff), 127, dtype=torch.int8, device=gpu)
+    w2 = torch.full((dff, dm), 127, dtype=torch.int8, device=gpu)
+    out, osc = ext.int8_mlp_forward(x, w1, w2, torch.full((T,), 1 / 127, device=gpu),
+                                    torch.full((dff,), 0.01 / 127, device=gpu),
+                                    torch.full((dm,), 0.01 / 127, device=gpu))
+    assert int(out.min()) == int(out.max()) == 127
+
+
+def test_mlp_argument_errors(ext, gpu):
+    x = torch.zeros(1, 4, 64, dtype=torch.int8, device=gpu)
+    w1 = torch.zeros(64, 128, dtype=torch.int8, device=gpu)
+    w2 = torch.zeros(128, 64, dtype=torch.int8, device=gpu)
+    with pytest.raises(RuntimeError, match="W1 shape mismatch"):
+        ext.int8_mlp_forward(x, w1[:32].contiguous(), w2, 1.0, 1.0, 1.0)
+    with pytest.raises(RuntimeError, match="x must be 3-D"):
+        ext.int8_mlp_forward(x[0], w1, w2, 1.0, 1.0, 1.0)
+    with pytest.raises(RuntimeError, match="scale_x must have 4"):
+        ext.int8_mlp_forward(x, w1, w2, torch.ones(3, device=gpu), torch.ones(128, device=gpu),
+                             torch.ones(64, device=gpu))
+    with pytest.raises(RuntimeError, match="multiples of 16"):
+        ext.int8_mlp_forward(torch.zeros(1, 4, 60, dtype=torch.int8, device=gpu),
+                             torch.zeros(60, 128, dtype=torch.int8, device=gpu),
+                             torch.zeros(128, 60, dtype=torch.int8, device=gpu), 1.0, 1.0, 1.0)
+
+
+def test_mlp_baseline_cfg4_full_size_sampled(ext, gpu):
+    # T=4096, 4096 -> 16384 -> 4096, per-token / per-channel.
+    T, dm, dff = 4096, 4096, 16384
+    c = workloads.mlp_case(T, dm, dff, seed=77, device=gpu)
+    W1T, W2T = ext.transpose_int8_weights(c["W1"], c["W2"])
+    out, osc = ext.int8_mlp_forward_prepacked(c["x"], W1T, W2T, c["sx"], c["sW1"], c["sW2"])
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(3).choice(T, size=12, replace=False)
+    x = _np(c["x"]).reshape(T, dm)[rows]
+    ref, rsc = O.mlp_forward(x, _np(c["W1"]), _np(c["W2"]), _np(c["sx"])[rows], _np(c["sW1"]),
+                             _np(c["sW2"]), gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out).reshape(T, dm)[rows], _np(osc)[rows], ref, rsc, "cfg4")
+    assert (np.abs(_np(out).astype(np.int32)).max(axis=-1) == 127).all()
+
+
+@pytest.fixture
+def capi_mlp(capi):
+    return capi
