@@ -78,6 +78,27 @@ int int8k_decode_attention_forward(
 int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
 
 /* ------------------------------------------------------------------------ */
+/* INT8 prefill attention (seq_q == seq_kv).                                 */
+/*                                                                          */
+/* Replaces int8_attention_forward(Q, K, V, out, scale_Q, scale_K, scale_V,  */
+/* batch, heads, seq_len, head_dim) — kernels/int8_attention.cu:926-929,     */
+/* declared at kernels/int8_ext.cu:27-31 — and adds `causal` (the reference  */
+/* is non-causal only; causal = 0 reproduces it).                            */
+/*                                                                          */
+/*   Q, K, V int8 [batch, heads, seq_len, head_dim]                          */
+/*   scale_Q/K/V fp32 [batch*heads*seq_len] (per token)                      */
+/*   out fp16 [batch, heads, seq_len, head_dim]                              */
+/*   s_ij = (q_i.k_j) sQ_i sK_j / sqrt(D);  out_i = sum_j softmax_j(s) v_j sV_j*/
+/*   causal: key j visible to query i iff j <= i.                            */
+/* head_dim must be 64, 128 or 256; seq_len >= 1.  Q, K, V 16-byte aligned,   */
+/* out 8-byte aligned.                                                       */
+/* ------------------------------------------------------------------------ */
+int int8k_attention_forward(
+    const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int batch, int heads, int seq_len, int head_dim, int causal, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* INT8 MLP: Linear -> GELU(tanh) -> Linear with dynamic per-token requant.  */
 /*                                                                          */
 /*   x  int8 [T, d_model]    W1 int8 [d_model, d_ff]   W2 int8 [d_ff, d_model]*/

@@ -52,6 +52,53 @@ torch::Tensor aligned_i8(const torch::Tensor& t) {
 
 }  // namespace
 
+// ── prefill attention (seq_q == seq_kv) ───────────────────────────────────
+// Mirrors int8_attention_forward_torch (kernels/int8_ext.cu:83-129): Q/K/V int8
+// (batch, heads, seq_len, head_dim), all the same shape; per-token fp32 scales
+// with batch*heads*seq_len elements; returns fp16 of Q's shape.  `is_causal`
+// is a new optional trailing argument (default false = the reference's math).
+torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                           torch::Tensor scale_Q, torch::Tensor scale_K,
+                                           torch::Tensor scale_V, bool is_causal) {
+    TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
+    TORCH_CHECK(Q.dtype() == torch::kInt8, "Q must be int8");
+    TORCH_CHECK(K.dtype() == torch::kInt8, "K must be int8");
+    TORCH_CHECK(V.dtype() == torch::kInt8, "V must be int8");
+    TORCH_CHECK(Q.is_contiguous(), "Q must be contiguous");
+    TORCH_CHECK(K.is_contiguous(), "K must be contiguous");
+    TORCH_CHECK(V.is_contiguous(), "V must be contiguous");
+    TORCH_CHECK(Q.dim() == 4, "expected (batch, heads, seq_len, head_dim)");
+    TORCH_CHECK(Q.sizes() == K.sizes() && Q.sizes() == V.sizes(), "Q/K/V shape mismatch");
+    TORCH_CHECK(scale_Q.dtype() == torch::kFloat32, "scale_Q must be float32");
+    TORCH_CHECK(scale_K.dtype() == torch::kFloat32, "scale_K must be float32");
+    TORCH_CHECK(scale_V.dtype() == torch::kFloat32, "scale_V must be float32");
+    TORCH_CHECK(scale_Q.device().is_cuda(), "scale_Q must be CUDA");
+    TORCH_CHECK(K.device() == Q.device() && V.device() == Q.device() &&
+                    scale_Q.device() == Q.device() && scale_K.device() == Q.device() &&
+                    scale_V.device() == Q.device(),
+                "all inputs must be on Q's device");
+    const int64_t batch = Q.size(0), heads = Q.size(1), seq_len = Q.size(2),
+                  head_dim = Q.size(3);
+    TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                "prefill attention supports head_dim 64, 128 or 256");
+    TORCH_CHECK(seq_len >= 1 && batch * heads * seq_len <= INT32_MAX, "seq_len out of range");
+    const int64_t n_tokens = batch * heads * seq_len;
+    auto sQ = scale_Q.contiguous().view({n_tokens});
+    auto sK = scale_K.contiguous().view({n_tokens});
+    auto sV = scale_V.contiguous().view({n_tokens});
+    auto q = aligned_i8(Q), k = aligned_i8(K), v = aligned_i8(V);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
+    auto out = torch::empty({batch, heads, seq_len, head_dim},
+                            torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
+    const int st = int8k_attention_forward(
+        q.data_ptr<int8_t>(), k.data_ptr<int8_t>(), v.data_ptr<int8_t>(),
+        reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
+        sK.data_ptr<float>(), sV.data_ptr<float>(), (int)batch, (int)heads, (int)seq_len,
+        (int)head_dim, is_causal ? 1 : 0, current_stream(Q));
+    check_status(st, "int8_attention_forward");
+    return out;
+}
+
 // ── decode attention (seq_q == 1) ─────────────────────────────────────────
 // Mirrors int8_decode_attention_forward_torch (kernels/int8_ext.cu:136-178).
 // Q : (batch, heads, head_dim) int8; K, V : (batch, heads, seq_kv, head_dim)
@@ -297,6 +344,10 @@ std::tuple<torch::Tensor, torch::Tensor> int8_mlp_forward_prepacked_pc_torch(
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("int8_attention_forward", &int8_attention_forward_torch,
+          "INT8 attention with per-token quantization — returns FP16 (optional is_causal)",
+          py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("scale_Q"), py::arg("scale_K"),
+          py::arg("scale_V"), py::arg("is_causal") = false);
     m.def("int8_decode_attention_forward", &int8_decode_attention_forward_torch,
           "INT8 flash-decoding attention (seq_q==1, INT8 KV cache) — returns FP16");
     // Two overloads: scalar scales (per-tensor) and tensor scales (per-token

@@ -1,0 +1,279 @@
+// prefill.hip — INT8 flash attention for prefill (seq_q == seq_kv), gfx950.
+//
+// Contract of the reference int8_attention_forward (kernels/int8_attention.cu:
+// 926-1028; math at kernels/int8_attention.cu:292-298, 467-643):
+//   s_ij  = (q_i . k_j) [exact int32] * sQ_i * sK_j / sqrt(D)
+//   p_ij  = softmax_j(s_ij)                          (fp32, online)
+//   out_i = sum_j (p_ij * sV_j)[fp16] * v_j[fp16] / sum_j p_ij   -> fp16
+// Non-causal by default (the reference has no mask); `causal` adds the
+// standard lower-triangular mask (key j visible to query i iff j <= i).
+//
+// Design (CDNA4): a block owns 128 queries of one (b,h), 4 waves x 32 queries,
+// and walks the KV sequence in tiles of 64 keys.  Everything is computed
+// transposed so that each lane owns one query:
+//   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows read
+//                                   straight from global/L1, B = Q kept in VGPRs)
+//   O^T[D x 32 q]      += V^T . P^T on v_mfma_f32_32x32x16_f16
+// In the 32x32 accumulator layout lane l holds column l%32 — its query — and
+// 16 of the 32 keys, so the row max, the exponentials, the running sum and the
+// rescale of O are lane-local except for one exchange with lane l^32, which
+// holds the other 16 keys of the same query.  P^T feeds the PV MFMA from the
+// registers it was computed in; V is staged once per tile into LDS as fp16 V^T
+// with the key order permuted to match those P^T registers, so each V^T
+// fragment is a single 16-byte LDS read.
+#include <cmath>
+
+#include "int8k_common.h"
+
+namespace int8k {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kQ = 128;        // queries per block
+constexpr int kKV = 64;        // keys per tile
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
+
+// LDS position of key kk (0..63) of a tile inside a V^T row: keys
+// 16t + 8a + 4h + c are stored at 16t + 8h + 4a + c, so the 8 keys that lane
+// half h of the PV B-operand holds for slice t are contiguous.
+__device__ __forceinline__ int vt_pos(int kk) {
+    const int t = kk >> 4, a = (kk >> 3) & 1, h = (kk >> 2) & 1, c = kk & 3;
+    return 16 * t + 8 * h + 4 * a + c;
+}
+
+// Stage V[k0 .. k0+63][0 .. D) (int8) into LDS as fp16 V^T[d][vt_pos(key)].
+// Work item: 4 keys x 4 dims; keys past S read a clamped row (their P is 0).
+template <int D>
+__device__ __forceinline__ void stage_vt(const int8_t* __restrict__ Vbh, int k0, int S,
+                                         _Float16* vt) {
+    constexpr int kDG = D / 4;
+    constexpr int kItems = (kKV / 4) * kDG;
+#pragma unroll
+    for (int it = threadIdx.x; it < kItems; it += kThreads) {
+        const int kg = it / kDG, dg = it % kDG;
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = min(k0 + 4 * kg + i, S - 1);
+            w[i] = *reinterpret_cast<const uint32_t*>(Vbh + (size_t)key * D + 4 * dg);
+        }
+        const int p0 = vt_pos(4 * kg);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            _Float16 h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                h[i] = (_Float16)(float)(int8_t)((w[i] >> (8 * j)) & 0xff);
+            typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<v4h*>(vt + (4 * dg + j) * kVtStride + p0) = v4h{h[0], h[1], h[2], h[3]};
+        }
+    }
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
+    const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
+    uint16_t* __restrict__ out, int S, int n_qtiles, float qk_scale_log2, bool vec_scales) {
+    constexpr int NS = D / 32;  // 32-wide d slices (QK k-steps) and O^T row tiles
+    __shared__ __align__(16) _Float16 vt[D * kVtStride];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int h = lane >> 5;
+    // heaviest (latest) query tiles first under the causal mask
+    const int bh = blockIdx.x / n_qtiles;
+    const int qt = CAUSAL ? n_qtiles - 1 - (int)(blockIdx.x % n_qtiles) : (int)(blockIdx.x % n_qtiles);
+    const int qw0 = qt * kQ + wave * 32;  // first query of this wave
+    const int q = qw0 + (lane & 31);      // this lane's query
+    const bool qok = q < S;
+
+    const size_t base = (size_t)bh * S;
+    const int8_t* Qbh = Q + base * D;
+    const int8_t* Kbh = K + base * D;
+    const int8_t* Vbh = V + base * D;
+    const float* sKbh = sK + base;
+    const float* sVbh = sV + base;
+
+    // Q^T fragments (B operand of the QK MFMA): column q, 16 bytes of d-slice s.
+    v4i qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        qf[s] = *reinterpret_cast<const v4i*>(Qbh + (size_t)min(q, S - 1) * D + 32 * s + 16 * h);
+    const float qscale = qok ? sQ[base + q] * qk_scale_log2 : 0.f;
+
+    v16f o[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+    float m = -INFINITY, lsum = 0.f;
+
+    const int q_block_end = min(S, (qt + 1) * kQ);
+    const int kv_end = CAUSAL ? q_block_end : S;
+    const int n_kv = (kv_end + kKV - 1) / kKV;
+    const int q_wave_last = min(qw0 + 31, S - 1);
+
+    for (int kt = 0; kt < n_kv; ++kt) {
+        const int k0 = kt * kKV;
+        __syncthreads();  // previous tile's V^T reads are done
+        stage_vt<D>(Vbh, k0, S, vt);
+        __syncthreads();
+        if (CAUSAL && k0 > q_wave_last) continue;  // whole tile masked for this wave
+
+        // S^T = K . Q^T for two 32-key tiles
+        v16i sacc[2];
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[T][r] = 0;
+            const int key = min(k0 + 32 * T + (lane & 31), S - 1);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const v4i kf =
+                    *reinterpret_cast<const v4i*>(Kbh + (size_t)key * D + 32 * s + 16 * h);
+                sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[s], sacc[T], 0, 0, 0);
+            }
+        }
+
+        // scores (log2 domain) for this lane's 32 keys: key = k0 + 32T + 8(r/4) + 4h + r%4
+        float sc[2][16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int kb = k0 + 32 * T + 8 * g + 4 * h;
+                float4 skv;
+                if (vec_scales && kb + 3 < S) {
+                    skv = *reinterpret_cast<const float4*>(sKbh + kb);
+                } else {
+                    skv.x = sKbh[min(kb, S - 1)];
+                    skv.y = sKbh[min(kb + 1, S - 1)];
+                    skv.z = sKbh[min(kb + 2, S - 1)];
+                    skv.w = sKbh[min(kb + 3, S - 1)];
+                }
+                const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int key = kb + c;
+                    float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
+                    const bool masked = key >= S || (CAUSAL && key > q);
+                    v = masked ? -INFINITY : v;
+                    sc[T][4 * g + c] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m, mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float corr = fast_exp2(m - m_use);
+        m = m_new;
+        lsum *= corr;
+#pragma unroll
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+
+        // P'^T fragments: slice t (16 keys) = registers r in [8(t%2), 8(t%2)+8) of tile t/2
+        v8h pf[4];
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int kb = k0 + 32 * T + 8 * g + 4 * h;
+                float4 svv;
+                if (vec_scales && kb + 3 < S) {
+                    svv = *reinterpret_cast<const float4*>(sVbh + kb);
+                } else {
+                    svv.x = sVbh[min(kb, S - 1)];
+                    svv.y = sVbh[min(kb + 1, S - 1)];
+                    svv.z = sVbh[min(kb + 2, S - 1)];
+                    svv.w = sVbh[min(kb + 3, S - 1)];
+                }
+                const float svk[4] = {svv.x, svv.y, svv.z, svv.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float p = fast_exp2(sc[T][4 * g + c] - m_use);
+                    lsum += p;
+                    pf[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
+                }
+            }
+
+        // O^T += V^T . P'^T
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const _Float16* row = vt + (32 * t + (lane & 31)) * kVtStride + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const v8h vf = *reinterpret_cast<const v8h*>(row + 16 * ks);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[t], 0, 0, 0);
+            }
+        }
+    }
+
+    const float L = lsum + __shfl_xor(lsum, 32);
+    if (!qok) return;
+    const float inv = 1.f / L;
+    uint16_t* orow = out + (base + q) * D;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * t + 8 * g + 4 * h;
+            const uint32_t lo = f32_to_f16_bits(o[t][4 * g] * inv) |
+                                ((uint32_t)f32_to_f16_bits(o[t][4 * g + 1] * inv) << 16);
+            const uint32_t hi = f32_to_f16_bits(o[t][4 * g + 2] * inv) |
+                                ((uint32_t)f32_to_f16_bits(o[t][4 * g + 3] * inv) << 16);
+            *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
+        }
+}
+
+template <int D>
+int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+                   const float* sQ, const float* sK, const float* sV, int BH, int S, bool causal,
+                   hipStream_t stream) {
+    const int n_qtiles = (S + kQ - 1) / kQ;
+    const long long blocks = (long long)BH * n_qtiles;
+    const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
+    // float4 scale loads need every (b,h) row of scales 16-byte aligned
+    const bool vec = (S % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
+    if (causal)
+        prefill_kernel<D, true><<<(unsigned)blocks, kThreads, 0, stream>>>(
+            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk, vec);
+    else
+        prefill_kernel<D, false><<<(unsigned)blocks, kThreads, 0, stream>>>(
+            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk, vec);
+    return check_launch("prefill_kernel");
+}
+
+}  // namespace
+}  // namespace int8k
+
+using namespace int8k;
+
+extern "C" int int8k_attention_forward(const int8_t* Q, const int8_t* K, const int8_t* V,
+                                       uint16_t* out, const float* scale_Q, const float* scale_K,
+                                       const float* scale_V, int batch, int heads, int seq_len,
+                                       int head_dim, int causal, void* stream) {
+    clear_last_error();
+    if (!Q || !K || !V || !out || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
+    const long long BH = (long long)batch * heads;
+    if (BH * ((seq_len + kQ - 1) / kQ) >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) || !aligned_to(out, 8) ||
+        !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
+        return INT8K_ERR_MISALIGNED;
+    hipStream_t s = as_stream(stream);
+    switch (head_dim) {
+        case 64: return launch_prefill<64>(Q, K, V, out, scale_Q, scale_K, scale_V, (int)BH, seq_len, causal != 0, s);
+        case 128: return launch_prefill<128>(Q, K, V, out, scale_Q, scale_K, scale_V, (int)BH, seq_len, causal != 0, s);
+        default: return launch_prefill<256>(Q, K, V, out, scale_Q, scale_K, scale_V, (int)BH, seq_len, causal != 0, s);
+    }
+}

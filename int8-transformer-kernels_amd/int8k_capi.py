@@ -43,6 +43,7 @@ _SIGNATURES = {
                                _P, _SZ, _P]),
     "int8k_transpose_int8_weights": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "int8k_gemm_i8_i32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "int8k_attention_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
 }
 
 MLP_WEIGHTS_PREPACKED = 1
@@ -187,3 +188,22 @@ def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, flags=0, out=None, out_scal
         _ptr(workspace), workspace.numel(), _stream(x))
     check("int8k_mlp_forward", st)
     return out, out_scale
+
+
+# --------------------------------------------------------------------------
+# prefill attention
+# --------------------------------------------------------------------------
+
+
+def attention_forward(Qi, Ki, Vi, sQ, sK, sV, causal=False, out=None):
+    """Q/K/V int8 [B,H,S,D] (device), per-token fp32 scales (B*H*S) -> fp16 [B,H,S,D]."""
+    import torch
+
+    B, H, S, D = Qi.shape
+    if out is None:
+        out = torch.empty((B, H, S, D), dtype=torch.float16, device=Qi.device)
+    st = load().int8k_attention_forward(_ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(out), _ptr(sQ),
+                                        _ptr(sK), _ptr(sV), B, H, S, D, int(bool(causal)),
+                                        _stream(Qi))
+    check("int8k_attention_forward", st)
+    return out
