@@ -46,49 +46,99 @@ __device__ __forceinline__ int vt_pos(int kk) {
     return 16 * t + 8 * h + 4 * a + c;
 }
 
-// Stage V[k0 .. k0+63][0 .. D) (int8) into LDS as fp16 V^T[d][vt_pos(key)].
-// Work item: 4 keys x 4 dims; keys past S read a clamped row (their P is 0).
+// One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16), scales.
 template <int D>
-__device__ __forceinline__ void stage_vt(const int8_t* __restrict__ Vbh, int k0, int S,
-                                         _Float16* vt) {
-    constexpr int kDG = D / 4;
-    constexpr int kItems = (kKV / 4) * kDG;
+struct Stage {
+    static constexpr int kKStride = D + 16;  // bytes per K row
+    static constexpr int kKBytes = kKV * kKStride;
+    static constexpr int kVtBytes = D * kVtStride * 2;
+    static constexpr int kBytes = kKBytes + kVtBytes + 2 * kKV * 4;
+    static constexpr int kKChunks = kKV * D / 16 / kThreads;       // 16-B K chunks per thread
+    static constexpr int kVItems = kKV * D / 16 / kThreads;        // 4x4 V blocks per thread
+};
+
+// Registers holding the next tile while the current one is computed.
+template <int D>
+struct Prefetch {
+    int4 k[Stage<D>::kKChunks];
+    uint32_t v[Stage<D>::kVItems][4];
+    float sc;  // threads 0..63: sK of key tid; 64..127: sV of key tid-64
+};
+
+template <int D>
+__device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const int8_t* __restrict__ Kbh,
+                                              const int8_t* __restrict__ Vbh,
+                                              const float* __restrict__ sKbh,
+                                              const float* __restrict__ sVbh, int k0, int S) {
+    const int t = threadIdx.x;
 #pragma unroll
-    for (int it = threadIdx.x; it < kItems; it += kThreads) {
-        const int kg = it / kDG, dg = it % kDG;
-        uint32_t w[4];
+    for (int n = 0; n < Stage<D>::kKChunks; ++n) {
+        const int c = t + n * kThreads;
+        const int row = c / (D / 16), col = (c % (D / 16)) * 16;
+        pf.k[n] = *reinterpret_cast<const int4*>(Kbh + (size_t)min(k0 + row, S - 1) * D + col);
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = min(k0 + 4 * kg + i, S - 1);
-            w[i] = *reinterpret_cast<const uint32_t*>(Vbh + (size_t)key * D + 4 * dg);
-        }
+    for (int n = 0; n < Stage<D>::kVItems; ++n) {
+        const int it = t + n * kThreads;
+        const int kg = it / (D / 4), dg = it % (D / 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            pf.v[n][i] = *reinterpret_cast<const uint32_t*>(
+                Vbh + (size_t)min(k0 + 4 * kg + i, S - 1) * D + 4 * dg);
+    }
+    if (t < 2 * kKV) {
+        const int key = min(k0 + (t & (kKV - 1)), S - 1);
+        pf.sc = t < kKV ? sKbh[key] : sVbh[key];
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
+    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int n = 0; n < Stage<D>::kKChunks; ++n) {
+        const int c = t + n * kThreads;
+        const int row = c / (D / 16), col = (c % (D / 16)) * 16;
+        *reinterpret_cast<int4*>(st + row * Stage<D>::kKStride + col) = pf.k[n];
+    }
+    _Float16* vt = reinterpret_cast<_Float16*>(st + Stage<D>::kKBytes);
+#pragma unroll
+    for (int n = 0; n < Stage<D>::kVItems; ++n) {
+        const int it = t + n * kThreads;
+        const int kg = it / (D / 4), dg = it % (D / 4);
         const int p0 = vt_pos(4 * kg);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             _Float16 h[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                h[i] = (_Float16)(float)(int8_t)((w[i] >> (8 * j)) & 0xff);
-            typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+                h[i] = (_Float16)(float)(int8_t)((pf.v[n][i] >> (8 * j)) & 0xff);
             *reinterpret_cast<v4h*>(vt + (4 * dg + j) * kVtStride + p0) = v4h{h[0], h[1], h[2], h[3]};
         }
     }
+    if (t < 2 * kKV)
+        reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(
+__global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
     const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
-    uint16_t* __restrict__ out, int S, int n_qtiles, float qk_scale_log2, bool vec_scales) {
+    uint16_t* __restrict__ out, int S, int n_qtiles, float qk_scale_log2) {
     constexpr int NS = D / 32;  // 32-wide d slices (QK k-steps) and O^T row tiles
-    __shared__ __align__(16) _Float16 vt[D * kVtStride];
+    using St = Stage<D>;
+    extern __shared__ __align__(16) char smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int h = lane >> 5;
-    // heaviest (latest) query tiles first under the causal mask
-    const int bh = blockIdx.x / n_qtiles;
-    const int qt = CAUSAL ? n_qtiles - 1 - (int)(blockIdx.x % n_qtiles) : (int)(blockIdx.x % n_qtiles);
+    // Under the causal mask a query tile's work grows with its index, so the
+    // grid is query-tile-major, heaviest tiles of every (b,h) first; without
+    // it, the query tiles of one (b,h) are adjacent (they share K/V in L2).
+    const int BH = gridDim.x / n_qtiles;
+    const int bh = CAUSAL ? (int)(blockIdx.x % BH) : (int)(blockIdx.x / n_qtiles);
+    const int qt = CAUSAL ? n_qtiles - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x % n_qtiles);
     const int qw0 = qt * kQ + wave * 32;  // first query of this wave
     const int q = qw0 + (lane & 31);      // this lane's query
     const bool qok = q < S;
@@ -119,102 +169,109 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     const int n_kv = (kv_end + kKV - 1) / kKV;
     const int q_wave_last = min(qw0 + 31, S - 1);
 
-    for (int kt = 0; kt < n_kv; ++kt) {
+    // Pipeline: tile kt is computed from LDS stage kt&1.  Two register sets
+    // (pa, pb) hold the next two tiles, so each tile's global loads have two
+    // tile-steps to land before they are committed to LDS at the end of the
+    // step that precedes their use; the step's only barrier follows the commit.
+    Prefetch<D> pa, pb;
+    prefetch_tile<D>(pa, Kbh, Vbh, sKbh, sVbh, 0, S);
+    commit_tile<D>(pa, smem);
+    if (n_kv > 1) prefetch_tile<D>(pa, Kbh, Vbh, sKbh, sVbh, kKV, S);
+    if (n_kv > 2) prefetch_tile<D>(pb, Kbh, Vbh, sKbh, sVbh, 2 * kKV, S);
+    __syncthreads();
+    auto step = [&](int kt, Prefetch<D>& cur_pf) {
         const int k0 = kt * kKV;
-        __syncthreads();  // previous tile's V^T reads are done
-        stage_vt<D>(Vbh, k0, S, vt);
+        const char* st = smem + (kt & 1) * St::kBytes;
+        const _Float16* vt = reinterpret_cast<const _Float16*>(st + St::kKBytes);
+        const float* sk_l = reinterpret_cast<const float*>(st + St::kKBytes + St::kVtBytes);
+        const float* sv_l = sk_l + kKV;
+        if (!(CAUSAL && k0 > q_wave_last)) {  // skip tiles wholly masked for this wave
+            // S^T = K . Q^T for the two 32-key halves of the tile
+            v16i sacc[2];
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[T][r] = 0;
+                const char* krow = st + (32 * T + (lane & 31)) * St::kKStride + 16 * h;
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const v4i kf = *reinterpret_cast<const v4i*>(krow + 32 * s);
+                    sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[s], sacc[T], 0, 0, 0);
+                }
+            }
+            // scores (log2 domain) of this lane's 32 keys:
+            // key = k0 + 32T + 8g + 4h + c  <->  sacc[T][4g + c]
+            const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
+            float sc[2][16];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
+                    const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
+                        if (!full) {
+                            const int key = k0 + 32 * T + 8 * g + 4 * h + c;
+                            if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
+                        }
+                        sc[T][4 * g + c] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m, mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            // rescale only when some lane's running max moved (rare after the first tiles)
+            if (__ballot(m_new != m)) {
+                const float corr = fast_exp2(m - m_use);
+                lsum *= corr;
+#pragma unroll
+                for (int t = 0; t < NS; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+            }
+            m = m_new;
+
+            // P'^T = p * sV (fp16): slice t = registers [8(t%2), 8(t%2)+8) of half t/2
+            v8h pfr[4];
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 svv = *reinterpret_cast<const float4*>(sv_l + 32 * T + 8 * g + 4 * h);
+                    const float svk[4] = {svv.x, svv.y, svv.z, svv.w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float p = fast_exp2(sc[T][4 * g + c] - m_use);
+                        lsum += p;
+                        pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
+                    }
+                }
+
+            // O^T += V^T . P'^T
+#pragma unroll
+            for (int t = 0; t < NS; ++t) {
+                const _Float16* row = vt + (32 * t + (lane & 31)) * kVtStride + 8 * h;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const v8h vf = *reinterpret_cast<const v8h*>(row + 16 * ks);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pfr[ks], o[t], 0, 0, 0);
+                }
+            }
+        }
+        if (kt + 1 < n_kv) {
+            commit_tile<D>(cur_pf, smem + ((kt + 1) & 1) * St::kBytes);
+            if (kt + 3 < n_kv) prefetch_tile<D>(cur_pf, Kbh, Vbh, sKbh, sVbh, k0 + 3 * kKV, S);
+        }
+        // tile kt+1 is in LDS and every wave is done reading stage kt&1
         __syncthreads();
-        if (CAUSAL && k0 > q_wave_last) continue;  // whole tile masked for this wave
-
-        // S^T = K . Q^T for two 32-key tiles
-        v16i sacc[2];
-#pragma unroll
-        for (int T = 0; T < 2; ++T) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[T][r] = 0;
-            const int key = min(k0 + 32 * T + (lane & 31), S - 1);
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const v4i kf =
-                    *reinterpret_cast<const v4i*>(Kbh + (size_t)key * D + 32 * s + 16 * h);
-                sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[s], sacc[T], 0, 0, 0);
-            }
-        }
-
-        // scores (log2 domain) for this lane's 32 keys: key = k0 + 32T + 8(r/4) + 4h + r%4
-        float sc[2][16];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int kb = k0 + 32 * T + 8 * g + 4 * h;
-                float4 skv;
-                if (vec_scales && kb + 3 < S) {
-                    skv = *reinterpret_cast<const float4*>(sKbh + kb);
-                } else {
-                    skv.x = sKbh[min(kb, S - 1)];
-                    skv.y = sKbh[min(kb + 1, S - 1)];
-                    skv.z = sKbh[min(kb + 2, S - 1)];
-                    skv.w = sKbh[min(kb + 3, S - 1)];
-                }
-                const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int key = kb + c;
-                    float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
-                    const bool masked = key >= S || (CAUSAL && key > q);
-                    v = masked ? -INFINITY : v;
-                    sc[T][4 * g + c] = v;
-                    mx = fmaxf(mx, v);
-                }
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m, mx);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float corr = fast_exp2(m - m_use);
-        m = m_new;
-        lsum *= corr;
-#pragma unroll
-        for (int t = 0; t < NS; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-
-        // P'^T fragments: slice t (16 keys) = registers r in [8(t%2), 8(t%2)+8) of tile t/2
-        v8h pf[4];
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int kb = k0 + 32 * T + 8 * g + 4 * h;
-                float4 svv;
-                if (vec_scales && kb + 3 < S) {
-                    svv = *reinterpret_cast<const float4*>(sVbh + kb);
-                } else {
-                    svv.x = sVbh[min(kb, S - 1)];
-                    svv.y = sVbh[min(kb + 1, S - 1)];
-                    svv.z = sVbh[min(kb + 2, S - 1)];
-                    svv.w = sVbh[min(kb + 3, S - 1)];
-                }
-                const float svk[4] = {svv.x, svv.y, svv.z, svv.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float p = fast_exp2(sc[T][4 * g + c] - m_use);
-                    lsum += p;
-                    pf[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
-                }
-            }
-
-        // O^T += V^T . P'^T
-#pragma unroll
-        for (int t = 0; t < NS; ++t) {
-            const _Float16* row = vt + (32 * t + (lane & 31)) * kVtStride + 8 * h;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const v8h vf = *reinterpret_cast<const v8h*>(row + 16 * ks);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[t], 0, 0, 0);
-            }
-        }
+    };
+    for (int kt = 0; kt < n_kv; kt += 2) {
+        step(kt, pa);
+        if (kt + 1 < n_kv) step(kt + 1, pb);
     }
 
     const float L = lsum + __shfl_xor(lsum, 32);
@@ -241,14 +298,26 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
     const int n_qtiles = (S + kQ - 1) / kQ;
     const long long blocks = (long long)BH * n_qtiles;
     const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
-    // float4 scale loads need every (b,h) row of scales 16-byte aligned
-    const bool vec = (S % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
+    const int lds = 2 * Stage<D>::kBytes;
+    static bool configured = false;  // > 64 KiB of LDS needs the attribute
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<D, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)prefill_kernel<D, false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) {
+            set_last_error("hipFuncSetAttribute", e);
+            return INT8K_ERR_HIP;
+        }
+        configured = true;
+    }
     if (causal)
-        prefill_kernel<D, true><<<(unsigned)blocks, kThreads, 0, stream>>>(
-            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk, vec);
+        prefill_kernel<D, true><<<(unsigned)blocks, kThreads, lds, stream>>>(
+            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk);
     else
-        prefill_kernel<D, false><<<(unsigned)blocks, kThreads, 0, stream>>>(
-            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk, vec);
+        prefill_kernel<D, false><<<(unsigned)blocks, kThreads, lds, stream>>>(
+            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk);
     return check_launch("prefill_kernel");
 }
 
