@@ -77,6 +77,18 @@ int int8k_decode_attention_forward(
 /* The split count the forward call uses for this shape (after clamping). */
 int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
 
+/* Decode over a preallocated KV cache: K_cache/V_cache int8 [BH, capacity, D],
+ * sK_cache/sV_cache fp32 [BH*capacity]; the first S positions of each (b,h)
+ * are attended (S <= capacity).  Same math and workspace as
+ * int8k_decode_attention_forward, which is the case capacity == S.  No
+ * counterpart in the reference (its decode needs a contiguous [B,H,S,D]
+ * tensor); pairs with int8k_kv_cache_append. */
+int int8k_decode_attention_forward_cache(
+    const int8_t* Q, const int8_t* K_cache, const int8_t* V_cache, uint16_t* out,
+    const float* scale_Q, const float* sK_cache, const float* sV_cache,
+    int BH, int S, int capacity, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* INT8 prefill attention (seq_q == seq_kv).                                 */
 /*                                                                          */
@@ -149,6 +161,46 @@ int int8k_transpose_int8_weights(const int8_t* W1, const int8_t* W2, int8_t* W1T
 /* be checked bit-exactly).  K % 16 == 0; A, Bt 16-byte aligned.             */
 int int8k_gemm_i8_i32(const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K,
                       void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Quantization.                                                            */
+/* ------------------------------------------------------------------------ */
+typedef enum int8k_dtype {
+    INT8K_DTYPE_F16 = 0,
+    INT8K_DTYPE_BF16 = 1,
+    INT8K_DTYPE_F32 = 2
+} int8k_dtype;
+
+/* Per-tensor fp16 -> int8: *d_scale (device) receives max(amax,1e-8)/127 and
+ * output[i] = rn(clamp(input[i] / scale)).  Replaces quantize_fp16_to_int8
+ * (kernels/quant_utils.cu:56-69, declared kernels/int8_common.cuh:51-55); the
+ * reference returns scale 0 and code -128 for an all-zero input, this one
+ * guards amax with 1e-8 as the reference's Python quantizers do. */
+int int8k_quantize_fp16_to_int8(const uint16_t* input, int8_t* output, float* d_scale,
+                                long long n, void* stream);
+
+/* output[i] = fp16(input[i] * scale) with a host-side scale.  Replaces
+ * dequantize_int8_to_fp16 (kernels/quant_utils.cu:72-77). */
+int int8k_dequantize_int8_to_fp16(const int8_t* input, uint16_t* output, float scale,
+                                  long long n, void* stream);
+
+/* Per-token (row) quantization of x [rows, cols] (fp16, bf16 or fp32):
+ * scales[r] = max(max_c |x[r,c]|, 1e-8)/127, q = rn(clamp(x / s, -128, 127)) —
+ * bit-identical to the reference's Python quantizer
+ * (validation/check_decode.py:42-47), which every caller runs before the
+ * attention and MLP ops.  No C counterpart in the reference. */
+int int8k_quantize_per_token(const void* x, int dtype, int8_t* q, float* scales,
+                             long long rows, int cols, void* stream);
+
+/* INT8 KV-cache append: quantizes n_new tokens per (b,h) of k_new/v_new
+ * [BH, n_new, head_dim] (fp16, bf16 or fp32) per token into rows
+ * pos .. pos+n_new-1 of K_cache/V_cache [BH, capacity, head_dim] and their
+ * scales sK_cache/sV_cache [BH*capacity].  The producer side of decode; no
+ * counterpart in the reference (its callers quantize the whole cache in
+ * PyTorch, validation/check_decode.py:42-47). */
+int int8k_kv_cache_append(const void* k_new, const void* v_new, int dtype,
+                          int8_t* K_cache, int8_t* V_cache, float* sK_cache, float* sV_cache,
+                          int BH, int n_new, int pos, int capacity, int head_dim, void* stream);
 
 #ifdef __cplusplus
 }

@@ -258,7 +258,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
     const int8_t* __restrict__ V, const float* __restrict__ sQ,
     const float* __restrict__ sK, const float* __restrict__ sV,
     float* __restrict__ part_ml, float* __restrict__ part_acc, uint16_t* __restrict__ out,
-    int S, int nsplit, int chunk, int units, float qk_scale_log2, int stagger) {
+    int S, int S_cap, int nsplit, int chunk, int units, float qk_scale_log2, int stagger) {
     using G = DecodeGeom<D, NS>;
     const int lane = threadIdx.x & 63;
     const int unit = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
@@ -274,10 +274,11 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
     const Int4 q = load16(Q + (size_t)bh * D + sub * 16);
     const float qscale = sQ[bh] * qk_scale_log2;
 
-    const int8_t* Kbh = K + (size_t)bh * S * D;
-    const int8_t* Vbh = V + (size_t)bh * S * D;
-    const float* sKbh = sK + (size_t)bh * S;
-    const float* sVbh = sV + (size_t)bh * S;
+    // (b,h) rows sit S_cap apart (the cache capacity); the first S are valid
+    const int8_t* Kbh = K + (size_t)bh * S_cap * D;
+    const int8_t* Vbh = V + (size_t)bh * S_cap * D;
+    const float* sKbh = sK + (size_t)bh * S_cap;
+    const float* sVbh = sV + (size_t)bh * S_cap;
 
     float m = -INFINITY, l = 0.f;
     float acc[16];
@@ -394,12 +395,12 @@ DecodeWorkspace carve(void* ws, long long units, int D) {
 template <int D, int NS, bool VEC, bool FINAL>
 void launch_split(int flags, int stagger, dim3 grid, hipStream_t stream, const int8_t* Q,
                   const int8_t* K, const int8_t* V, const float* sQ, const float* sK,
-                  const float* sV, const DecodeWorkspace& w, uint16_t* out, int S,
+                  const float* sV, const DecodeWorkspace& w, uint16_t* out, int S, int S_cap,
                   const SplitPlan& plan, int units, float qk) {
-#define INT8K_SPLIT_LAUNCH(FLV)                                                               \
-    decode_split_kernel<D, NS, VEC, FINAL, FLV><<<grid, kBlockThreads, 0, stream>>>(          \
-        Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, out, S, plan.nsplit, plan.chunk, units, qk, \
-        stagger)
+#define INT8K_SPLIT_LAUNCH(FLV)                                                      \
+    decode_split_kernel<D, NS, VEC, FINAL, FLV><<<grid, kBlockThreads, 0, stream>>>( \
+        Q, K, V, sQ, sK, sV, w.part_ml, w.part_acc, out, S, S_cap, plan.nsplit,      \
+        plan.chunk, units, qk, stagger)
     switch (flags & 3) {
         case 0: INT8K_SPLIT_LAUNCH(0); break;
         case 1: INT8K_SPLIT_LAUNCH(1); break;
@@ -413,23 +414,23 @@ template <int D, bool VEC, bool FINAL>
 void launch_split_ns(int ns, int flags, int stagger, dim3 grid, hipStream_t stream,
                      const int8_t* Q, const int8_t* K, const int8_t* V, const float* sQ,
                      const float* sK, const float* sV, const DecodeWorkspace& w, uint16_t* out,
-                     int S, const SplitPlan& plan, int units, float qk) {
+                     int S, int S_cap, const SplitPlan& plan, int units, float qk) {
     if (ns == 4)
         launch_split<D, 4, VEC, FINAL>(flags, stagger, grid, stream, Q, K, V, sQ, sK, sV, w, out,
-                                       S, plan, units, qk);
+                                       S, S_cap, plan, units, qk);
     else
         launch_split<D, 8, VEC, FINAL>(flags, stagger, grid, stream, Q, K, V, sQ, sK, sV, w, out,
-                                       S, plan, units, qk);
+                                       S, S_cap, plan, units, qk);
 }
 
 template <int D>
 int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
-                  const float* sQ, const float* sK, const float* sV, int BH, int S,
+                  const float* sQ, const float* sK, const float* sV, int BH, int S, int S_cap,
                   const SplitPlan& plan, const DecodeWorkspace& w, hipStream_t stream) {
     const long long units = (long long)BH * plan.nsplit;
     const float qk_scale_log2 = (1.0f / std::sqrt((float)D)) * kLog2e;
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
-    const bool vec = (S % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
+    const bool vec = (S_cap % 4 == 0) && aligned_to(sK, 16) && aligned_to(sV, 16);
     const DecodeTuning tn = tuning_for(D);
     const int ns = tn.slots;
     const int fl = tn.flags;
@@ -438,13 +439,13 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     const float qk = qk_scale_log2;
     const bool final_pass = plan.nsplit == 1 && aligned_to(out, 16);
     if (vec && final_pass)
-        launch_split_ns<D, true, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
+        launch_split_ns<D, true, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, S_cap, plan, u, qk);
     else if (vec)
-        launch_split_ns<D, true, false>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
+        launch_split_ns<D, true, false>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, S_cap, plan, u, qk);
     else if (final_pass)
-        launch_split_ns<D, false, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
+        launch_split_ns<D, false, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, S_cap, plan, u, qk);
     else
-        launch_split_ns<D, false, false>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, plan, u, qk);
+        launch_split_ns<D, false, false>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, S_cap, plan, u, qk);
     int st = check_launch("decode_split_kernel");
     if (st != INT8K_OK || final_pass) return st;
     const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));
@@ -469,14 +470,13 @@ extern "C" size_t int8k_decode_attention_workspace_bytes(int BH, int S, int head
     return carve(nullptr, (long long)BH * plan.nsplit, head_dim).bytes;
 }
 
-extern "C" int int8k_decode_attention_forward(
-    const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
-    const float* scale_Q, const float* scale_K, const float* scale_V,
-    int BH, int S, int head_dim, int nsplit,
-    void* workspace, size_t workspace_bytes, void* stream) {
+static int decode_impl(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+                       const float* scale_Q, const float* scale_K, const float* scale_V, int BH,
+                       int S, int S_cap, int head_dim, int nsplit, void* workspace,
+                       size_t workspace_bytes, void* stream) {
     clear_last_error();
     if (!Q || !K || !V || !out || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
-    if (BH <= 0 || S <= 0 || nsplit < 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (BH <= 0 || S <= 0 || S_cap < S || nsplit < 0) return INT8K_ERR_INVALID_ARGUMENT;
     if (head_dim != 64 && head_dim != 128) return INT8K_ERR_UNSUPPORTED;
     if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) ||
         !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4) ||
@@ -489,8 +489,26 @@ extern "C" int int8k_decode_attention_forward(
     if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
     if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;
     if (head_dim == 128)
-        return launch_decode<128>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, plan, w,
-                                  as_stream(stream));
-    return launch_decode<64>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, plan, w,
+        return launch_decode<128>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, S_cap, plan,
+                                  w, as_stream(stream));
+    return launch_decode<64>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, S_cap, plan, w,
                              as_stream(stream));
+}
+
+extern "C" int int8k_decode_attention_forward(
+    const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int BH, int S, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    return decode_impl(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, S, head_dim, nsplit,
+                       workspace, workspace_bytes, stream);
+}
+
+extern "C" int int8k_decode_attention_forward_cache(
+    const int8_t* Q, const int8_t* K_cache, const int8_t* V_cache, uint16_t* out,
+    const float* scale_Q, const float* sK_cache, const float* sV_cache,
+    int BH, int S, int capacity, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    return decode_impl(Q, K_cache, V_cache, out, scale_Q, sK_cache, sV_cache, BH, S, capacity,
+                       head_dim, nsplit, workspace, workspace_bytes, stream);
 }

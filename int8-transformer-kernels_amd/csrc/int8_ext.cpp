@@ -343,6 +343,151 @@ std::tuple<torch::Tensor, torch::Tensor> int8_mlp_forward_prepacked_pc_torch(
                    scale_W2.contiguous(), c10::nullopt, d, INT8K_MLP_WEIGHTS_PREPACKED);
 }
 
+// ── quantization and the INT8 KV cache (new ops; the reference exposes its
+// quant utils only as C++ functions, kernels/int8_common.cuh:51-59) ─────────
+
+namespace {
+
+int dtype_code(const torch::Tensor& t) {
+    if (t.dtype() == torch::kFloat16) return INT8K_DTYPE_F16;
+    if (t.dtype() == torch::kBFloat16) return INT8K_DTYPE_BF16;
+    if (t.dtype() == torch::kFloat32) return INT8K_DTYPE_F32;
+    TORCH_CHECK(false, "expected a float16, bfloat16 or float32 tensor");
+    return -1;
+}
+
+}  // namespace
+
+// Per-tensor fp16 -> int8 (kernels/quant_utils.cu:56-69): returns (int8, scale [1]).
+std::tuple<torch::Tensor, torch::Tensor> quantize_fp16_to_int8_torch(torch::Tensor x) {
+    TORCH_CHECK(x.device().is_cuda(), "x must be a CUDA tensor");
+    TORCH_CHECK(x.dtype() == torch::kFloat16, "x must be float16");
+    TORCH_CHECK(x.numel() > 0, "x must not be empty");
+    auto xc = x.contiguous();
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+    auto q = torch::empty(x.sizes(), torch::TensorOptions().dtype(torch::kInt8).device(x.device()));
+    auto s = torch::empty({1}, torch::TensorOptions().dtype(torch::kFloat32).device(x.device()));
+    check_status(int8k_quantize_fp16_to_int8(
+                     reinterpret_cast<const uint16_t*>(xc.data_ptr<at::Half>()), q.data_ptr<int8_t>(),
+                     s.data_ptr<float>(), xc.numel(), current_stream(x)),
+                 "quantize_fp16_to_int8");
+    return {q, s};
+}
+
+// int8 -> fp16 with a host scale (kernels/quant_utils.cu:72-77).
+torch::Tensor dequantize_int8_to_fp16_torch(torch::Tensor q, double scale) {
+    TORCH_CHECK(q.device().is_cuda(), "q must be a CUDA tensor");
+    TORCH_CHECK(q.dtype() == torch::kInt8, "q must be int8");
+    TORCH_CHECK(q.numel() > 0, "q must not be empty");
+    auto qc = q.contiguous();
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+    auto y = torch::empty(q.sizes(), torch::TensorOptions().dtype(torch::kFloat16).device(q.device()));
+    check_status(int8k_dequantize_int8_to_fp16(qc.data_ptr<int8_t>(),
+                                               reinterpret_cast<uint16_t*>(y.data_ptr<at::Half>()),
+                                               (float)scale, qc.numel(), current_stream(q)),
+                 "dequantize_int8_to_fp16");
+    return y;
+}
+
+// Per-token (last-dim) symmetric quantization: returns (int8 like x, fp32 x.shape[:-1]).
+std::tuple<torch::Tensor, torch::Tensor> quantize_per_token_torch(torch::Tensor x) {
+    TORCH_CHECK(x.device().is_cuda(), "x must be a CUDA tensor");
+    TORCH_CHECK(x.dim() >= 1 && x.numel() > 0, "x must be a non-empty tensor");
+    const int code = dtype_code(x);
+    auto xc = x.contiguous();
+    const int64_t cols = x.size(-1);
+    TORCH_CHECK(cols <= INT32_MAX, "rows too long");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+    auto q = torch::empty(x.sizes(), torch::TensorOptions().dtype(torch::kInt8).device(x.device()));
+    auto s = torch::empty(x.sizes().slice(0, x.dim() - 1),
+                          torch::TensorOptions().dtype(torch::kFloat32).device(x.device()));
+    check_status(int8k_quantize_per_token(xc.data_ptr(), code, q.data_ptr<int8_t>(),
+                                          s.data_ptr<float>(), xc.numel() / cols, (int)cols,
+                                          current_stream(x)),
+                 "quantize_per_token");
+    return {q, s};
+}
+
+// Quantize k_new/v_new (batch, heads, n_new, head_dim) per token into positions
+// pos .. pos+n_new-1 of the int8 caches (batch, heads, capacity, head_dim) and
+// their fp32 scales (batch, heads, capacity).  In place.
+void kv_cache_append_torch(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor K_cache,
+                           torch::Tensor V_cache, torch::Tensor sK_cache, torch::Tensor sV_cache,
+                           int64_t pos) {
+    TORCH_CHECK(k_new.device().is_cuda(), "k_new must be a CUDA tensor");
+    TORCH_CHECK(k_new.dim() == 4 && k_new.sizes() == v_new.sizes(),
+                "k_new/v_new must be (batch, heads, n_new, head_dim) of one shape");
+    TORCH_CHECK(k_new.dtype() == v_new.dtype(), "k_new/v_new dtype mismatch");
+    const int code = dtype_code(k_new);
+    TORCH_CHECK(K_cache.dtype() == torch::kInt8 && V_cache.dtype() == torch::kInt8,
+                "caches must be int8");
+    TORCH_CHECK(sK_cache.dtype() == torch::kFloat32 && sV_cache.dtype() == torch::kFloat32,
+                "cache scales must be float32");
+    TORCH_CHECK(K_cache.is_contiguous() && V_cache.is_contiguous() && sK_cache.is_contiguous() &&
+                    sV_cache.is_contiguous(),
+                "caches must be contiguous");
+    TORCH_CHECK(K_cache.dim() == 4 && K_cache.sizes() == V_cache.sizes(),
+                "caches must be (batch, heads, capacity, head_dim) of one shape");
+    const int64_t B = k_new.size(0), H = k_new.size(1), n = k_new.size(2), D = k_new.size(3);
+    const int64_t cap = K_cache.size(2);
+    TORCH_CHECK(K_cache.size(0) == B && K_cache.size(1) == H && K_cache.size(3) == D,
+                "cache/new-token shape mismatch");
+    TORCH_CHECK(sK_cache.numel() == B * H * cap && sV_cache.numel() == B * H * cap,
+                "cache scales must have batch*heads*capacity elements");
+    TORCH_CHECK(pos >= 0 && pos + n <= cap, "append past the cache capacity");
+    for (const auto* t : {&v_new, &K_cache, &V_cache, &sK_cache, &sV_cache})
+        TORCH_CHECK(t->device() == k_new.device(), "all tensors must be on one device");
+    auto kc = k_new.contiguous(), vc = v_new.contiguous();
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(k_new.device());
+    check_status(int8k_kv_cache_append(kc.data_ptr(), vc.data_ptr(), code, K_cache.data_ptr<int8_t>(),
+                                       V_cache.data_ptr<int8_t>(), sK_cache.data_ptr<float>(),
+                                       sV_cache.data_ptr<float>(), (int)(B * H), (int)n, (int)pos,
+                                       (int)cap, (int)D, current_stream(k_new)),
+                 "kv_cache_append");
+}
+
+// Decode over the first seq_len positions of a preallocated cache
+// (batch, heads, capacity, head_dim); Q (batch, heads, head_dim) int8.
+torch::Tensor int8_decode_attention_forward_cache_torch(torch::Tensor Q, torch::Tensor K_cache,
+                                                        torch::Tensor V_cache, torch::Tensor scale_Q,
+                                                        torch::Tensor sK_cache,
+                                                        torch::Tensor sV_cache, int64_t seq_len) {
+    TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
+    TORCH_CHECK(Q.dtype() == torch::kInt8 && K_cache.dtype() == torch::kInt8 &&
+                    V_cache.dtype() == torch::kInt8,
+                "Q/K/V must be int8");
+    TORCH_CHECK(Q.is_contiguous() && K_cache.is_contiguous() && V_cache.is_contiguous(),
+                "Q/K/V must be contiguous");
+    TORCH_CHECK(Q.dim() == 3 && K_cache.dim() == 4 && K_cache.sizes() == V_cache.sizes(),
+                "expected Q (batch, heads, head_dim), caches (batch, heads, capacity, head_dim)");
+    const int64_t B = Q.size(0), H = Q.size(1), D = Q.size(2), cap = K_cache.size(2);
+    TORCH_CHECK(K_cache.size(0) == B && K_cache.size(1) == H && K_cache.size(3) == D,
+                "Q/K head/batch/dim mismatch");
+    TORCH_CHECK(D == 64 || D == 128, "decode kernel v1 supports head_dim 64 or 128");
+    TORCH_CHECK(seq_len >= 1 && seq_len <= cap, "seq_len must be in [1, capacity]");
+    TORCH_CHECK(scale_Q.dtype() == torch::kFloat32 && sK_cache.dtype() == torch::kFloat32 &&
+                    sV_cache.dtype() == torch::kFloat32,
+                "scales must be float32");
+    TORCH_CHECK(sK_cache.numel() == B * H * cap && sV_cache.numel() == B * H * cap &&
+                    scale_Q.numel() == B * H,
+                "scale sizes mismatch");
+    auto sQ = scale_Q.contiguous();
+    auto sK = sK_cache.contiguous();
+    auto sV = sV_cache.contiguous();
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
+    auto out = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
+    const int BH = (int)(B * H);
+    const size_t ws_bytes = int8k_decode_attention_workspace_bytes(BH, (int)seq_len, (int)D, 0);
+    auto ws = workspace(ws_bytes, Q.device());
+    const int st = int8k_decode_attention_forward_cache(
+        Q.data_ptr<int8_t>(), K_cache.data_ptr<int8_t>(), V_cache.data_ptr<int8_t>(),
+        reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
+        sK.data_ptr<float>(), sV.data_ptr<float>(), BH, (int)seq_len, (int)cap, (int)D, 0,
+        ws.data_ptr(), ws_bytes, current_stream(Q));
+    check_status(st, "int8_decode_attention_forward_cache");
+    return out;
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("int8_attention_forward", &int8_attention_forward_torch,
           "INT8 attention with per-token quantization — returns FP16 (optional is_causal)",
@@ -366,5 +511,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("int8_mlp_forward_prepacked", &int8_mlp_forward_prepacked_pc_torch,
           "INT8 MLP, per-token/per-channel scales, pre-transposed weights — "
           "returns (int8_out, out_scale[T])");
+    // Not in the reference's module: quant utils it keeps C++-only, the
+    // per-token quantizer every caller runs in PyTorch, and the KV cache.
+    m.def("quantize_fp16_to_int8", &quantize_fp16_to_int8_torch,
+          "Per-tensor fp16 -> int8 — returns (int8, scale[1])");
+    m.def("dequantize_int8_to_fp16", &dequantize_int8_to_fp16_torch,
+          "int8 -> fp16 with a scalar scale");
+    m.def("quantize_per_token", &quantize_per_token_torch,
+          "Per-token (last dim) int8 quantization — returns (int8, fp32 scales)");
+    m.def("kv_cache_append", &kv_cache_append_torch,
+          "Quantize new K/V tokens into an int8 KV cache at position pos (in place)");
+    m.def("int8_decode_attention_forward_cache", &int8_decode_attention_forward_cache_torch,
+          "INT8 decode attention over the first seq_len positions of a KV cache — returns FP16");
     m.attr("abi_version") = int8k_abi_version();
 }

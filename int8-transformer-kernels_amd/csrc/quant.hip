@@ -1,0 +1,192 @@
+// quant.hip — quantization kernels: the reference's per-tensor quant utils and
+// the per-token quantizer / INT8 KV-cache append that feed the attention paths.
+//
+//   per-tensor (kernels/quant_utils.cu:12-77):
+//     amax = max|x| ; scale = max(amax, 1e-8) / 127 ; q = rn(clamp(x / scale))
+//     dequant: half(q * scale)
+//   The 1e-8 guard is deliberate: the reference kernel computes scale 0 on an
+//   all-zero input and returns code -128 (kernels/quant_utils.cu:29-31,
+//   39-40); every Python quantizer of the reference clamps amax to 1e-8.
+//   per-token (validation/check_decode.py:42-47, tests/test_int8.py:47-63):
+//     s_row = max(amax_row, 1e-8) / 127 ; q = rn(clamp(x / s_row, -128, 127))
+//   Division (not a reciprocal multiply) and round-half-even keep the codes
+//   bit-identical to torch's `(x.float() / s).round().clamp(-128, 127)`.
+#include "int8k_common.h"
+
+namespace int8k {
+namespace {
+
+__device__ __forceinline__ float load_elem(const void* p, size_t i, int dtype) {
+    switch (dtype) {
+        case INT8K_DTYPE_F16: return __half2float(reinterpret_cast<const __half*>(p)[i]);
+        case INT8K_DTYPE_BF16: {
+            const uint32_t b = reinterpret_cast<const uint16_t*>(p)[i];
+            return __uint_as_float(b << 16);
+        }
+        default: return reinterpret_cast<const float*>(p)[i];
+    }
+}
+
+__device__ __forceinline__ int8_t quant_div(float x, float s) {
+    return (int8_t)(int)__builtin_rintf(fminf(fmaxf(x / s, -128.f), 127.f));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+// ---------------------------------------------------------------- per tensor
+
+__global__ void zero_f32_kernel(float* p) { *p = 0.f; }
+
+__global__ __launch_bounds__(256) void amax_f16_kernel(const __half* __restrict__ x, size_t n,
+                                                       float* __restrict__ amax) {
+    __shared__ float red[4];
+    float m = 0.f;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        m = fmaxf(m, fabsf(__half2float(x[i])));
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        atomicMax(reinterpret_cast<int*>(amax), __float_as_int(m));  // m >= 0
+    }
+}
+
+// Reads the tensor amax left in *scale by amax_f16_kernel; every block derives
+// the same scale from it.
+__global__ __launch_bounds__(256) void quant_tensor_f16_kernel(const __half* __restrict__ x,
+                                                               int8_t* __restrict__ q, size_t n,
+                                                               const float* __restrict__ amax) {
+    const float s = fmaxf(*amax, 1e-8f) / 127.f;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        q[i] = quant_div(__half2float(x[i]), s);
+}
+
+__global__ void finalize_scale_kernel(float* scale) { *scale = fmaxf(*scale, 1e-8f) / 127.f; }
+
+__global__ __launch_bounds__(256) void dequant_f16_kernel(const int8_t* __restrict__ q,
+                                                          __half* __restrict__ y, size_t n,
+                                                          float scale) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        y[i] = __float2half_rn((float)q[i] * scale);
+}
+
+// ---------------------------------------------------------------- per token
+
+// One wave per row: amax pass, then the quantize pass (the row is re-read
+// from cache).  `dst_row(r)` maps source row r to its destination row, which
+// is how the KV-cache append scatters new tokens into the cache.
+struct RowMap {
+    long long rows_per_group;  // source rows per (b,h) group (1 group: all rows)
+    long long dst_group_stride;  // destination rows per group (cache capacity)
+    long long dst_offset;      // first destination row inside a group
+};
+
+__device__ __forceinline__ long long map_row(long long r, const RowMap& m) {
+    const long long g = r / m.rows_per_group, i = r - g * m.rows_per_group;
+    return g * m.dst_group_stride + m.dst_offset + i;
+}
+
+__global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict__ x, int dtype,
+                                                         int8_t* __restrict__ q,
+                                                         float* __restrict__ scales,
+                                                         long long rows, int cols, RowMap map) {
+    const long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const size_t src = (size_t)r * cols;
+    float m = 0.f;
+    for (int c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_elem(x, src + c, dtype)));
+    m = wave_max(m);
+    const float s = fmaxf(m, 1e-8f) / 127.f;
+    const long long d = map_row(r, map);
+    int8_t* qr = q + (size_t)d * cols;
+    for (int c = lane; c < cols; c += 64) qr[c] = quant_div(load_elem(x, src + c, dtype), s);
+    if (lane == 0) scales[d] = s;
+}
+
+int launch_quant_rows(const void* x, int dtype, int8_t* q, float* scales, long long rows,
+                      int cols, const RowMap& map, hipStream_t stream) {
+    const long long blocks = (rows + 3) / 4;
+    if (blocks >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    quant_rows_kernel<<<(unsigned)blocks, 256, 0, stream>>>(x, dtype, q, scales, rows, cols, map);
+    return check_launch("quant_rows_kernel");
+}
+
+inline int grid_for(long long n) {
+    const long long b = (n + 255) / 256;
+    return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
+}
+
+}  // namespace
+}  // namespace int8k
+
+using namespace int8k;
+
+extern "C" int int8k_quantize_fp16_to_int8(const uint16_t* input, int8_t* output, float* d_scale,
+                                           long long n, void* stream) {
+    clear_last_error();
+    if (!input || !output || !d_scale || n <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (!aligned_to(input, 2) || !aligned_to(d_scale, 4)) return INT8K_ERR_MISALIGNED;
+    hipStream_t s = as_stream(stream);
+    const __half* x = reinterpret_cast<const __half*>(input);
+    zero_f32_kernel<<<1, 1, 0, s>>>(d_scale);
+    int st = check_launch("zero_f32_kernel");
+    if (st != INT8K_OK) return st;
+    amax_f16_kernel<<<grid_for(n), 256, 0, s>>>(x, (size_t)n, d_scale);
+    if ((st = check_launch("amax_f16_kernel")) != INT8K_OK) return st;
+    quant_tensor_f16_kernel<<<grid_for(n), 256, 0, s>>>(x, output, (size_t)n, d_scale);
+    if ((st = check_launch("quant_tensor_f16_kernel")) != INT8K_OK) return st;
+    finalize_scale_kernel<<<1, 1, 0, s>>>(d_scale);
+    return check_launch("finalize_scale_kernel");
+}
+
+extern "C" int int8k_dequantize_int8_to_fp16(const int8_t* input, uint16_t* output, float scale,
+                                             long long n, void* stream) {
+    clear_last_error();
+    if (!input || !output || n <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (!aligned_to(output, 2)) return INT8K_ERR_MISALIGNED;
+    dequant_f16_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(
+        input, reinterpret_cast<__half*>(output), (size_t)n, scale);
+    return check_launch("dequant_f16_kernel");
+}
+
+extern "C" int int8k_quantize_per_token(const void* x, int dtype, int8_t* q, float* scales,
+                                        long long rows, int cols, void* stream) {
+    clear_last_error();
+    if (!x || !q || !scales || rows <= 0 || cols <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (!aligned_to(x, dtype == INT8K_DTYPE_F32 ? 4 : 2) || !aligned_to(scales, 4))
+        return INT8K_ERR_MISALIGNED;
+    return launch_quant_rows(x, dtype, q, scales, rows, cols, RowMap{rows, rows, 0},
+                             as_stream(stream));
+}
+
+extern "C" int int8k_kv_cache_append(const void* k_new, const void* v_new, int dtype,
+                                     int8_t* K_cache, int8_t* V_cache, float* sK_cache,
+                                     float* sV_cache, int BH, int n_new, int pos, int capacity,
+                                     int head_dim, void* stream) {
+    clear_last_error();
+    if (!k_new || !v_new || !K_cache || !V_cache || !sK_cache || !sV_cache)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (BH <= 0 || n_new <= 0 || pos < 0 || capacity <= 0 || head_dim <= 0)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if ((long long)pos + n_new > capacity) return INT8K_ERR_INVALID_ARGUMENT;
+    if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    const size_t ea = dtype == INT8K_DTYPE_F32 ? 4 : 2;
+    if (!aligned_to(k_new, ea) || !aligned_to(v_new, ea) || !aligned_to(sK_cache, 4) ||
+        !aligned_to(sV_cache, 4))
+        return INT8K_ERR_MISALIGNED;
+    const RowMap map{n_new, capacity, pos};
+    const long long rows = (long long)BH * n_new;
+    hipStream_t s = as_stream(stream);
+    int st = launch_quant_rows(k_new, dtype, K_cache, sK_cache, rows, head_dim, map, s);
+    if (st != INT8K_OK) return st;
+    return launch_quant_rows(v_new, dtype, V_cache, sV_cache, rows, head_dim, map, s);
+}

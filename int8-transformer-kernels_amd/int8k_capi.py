@@ -44,7 +44,15 @@ _SIGNATURES = {
     "int8k_transpose_int8_weights": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "int8k_gemm_i8_i32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "int8k_attention_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "int8k_decode_attention_forward_cache": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                                                  _P, _SZ, _P]),
+    "int8k_quantize_fp16_to_int8": (_I, [_P, _P, _P, _LL, _P]),
+    "int8k_dequantize_int8_to_fp16": (_I, [_P, _P, _F, _LL, _P]),
+    "int8k_quantize_per_token": (_I, [_P, _I, _P, _P, _LL, _I, _P]),
+    "int8k_kv_cache_append": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
 }
+
+DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 
 MLP_WEIGHTS_PREPACKED = 1
 MLP_OUT_PER_TENSOR = 2
@@ -206,4 +214,80 @@ def attention_forward(Qi, Ki, Vi, sQ, sK, sV, causal=False, out=None):
                                         _ptr(sK), _ptr(sV), B, H, S, D, int(bool(causal)),
                                         _stream(Qi))
     check("int8k_attention_forward", st)
+    return out
+
+
+# --------------------------------------------------------------------------
+# quantization and the KV cache
+# --------------------------------------------------------------------------
+
+
+def _dtype_code(t):
+    import torch
+
+    codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+    if t.dtype not in codes:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    return codes[t.dtype]
+
+
+def quantize_fp16_to_int8(x):
+    """Per-tensor: returns (int8 codes, fp32 device scale [1])."""
+    import torch
+
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(1, dtype=torch.float32, device=x.device)
+    check("int8k_quantize_fp16_to_int8",
+          load().int8k_quantize_fp16_to_int8(_ptr(x), _ptr(q), _ptr(s), x.numel(), _stream(x)))
+    return q, s
+
+
+def dequantize_int8_to_fp16(q, scale: float):
+    import torch
+
+    y = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    check("int8k_dequantize_int8_to_fp16",
+          load().int8k_dequantize_int8_to_fp16(_ptr(q), _ptr(y), float(scale), q.numel(),
+                                               _stream(q)))
+    return y
+
+
+def quantize_per_token(x):
+    """Rows of the last dim: returns (int8 codes like x, fp32 scales x.shape[:-1])."""
+    import torch
+
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    check("int8k_quantize_per_token",
+          load().int8k_quantize_per_token(_ptr(x), _dtype_code(x), _ptr(q), _ptr(s), rows, cols,
+                                          _stream(x)))
+    return q, s
+
+
+def kv_cache_append(k_new, v_new, K_cache, V_cache, sK_cache, sV_cache, pos: int):
+    """k_new/v_new [B,H,n,D]; caches [B,H,cap,D] int8 and [B,H,cap] fp32."""
+    B, H, n, D = k_new.shape
+    cap = K_cache.shape[2]
+    check("int8k_kv_cache_append",
+          load().int8k_kv_cache_append(_ptr(k_new), _ptr(v_new), _dtype_code(k_new),
+                                       _ptr(K_cache), _ptr(V_cache), _ptr(sK_cache),
+                                       _ptr(sV_cache), B * H, n, pos, cap, D, _stream(k_new)))
+
+
+def decode_attention_cache(Qi, K_cache, V_cache, sQ, sK_cache, sV_cache, S, nsplit=0, out=None):
+    """Decode over the first S positions of a [B,H,cap,D] cache."""
+    import torch
+
+    B, H, cap, D = K_cache.shape
+    BH = B * H
+    if out is None:
+        out = torch.empty((BH, D), dtype=torch.float16, device=Qi.device)
+    ws = torch.empty(max(decode_workspace_bytes(BH, S, D, nsplit), 1), dtype=torch.uint8,
+                     device=Qi.device)
+    st = load().int8k_decode_attention_forward_cache(
+        _ptr(Qi), _ptr(K_cache), _ptr(V_cache), _ptr(out), _ptr(sQ), _ptr(sK_cache),
+        _ptr(sV_cache), BH, S, cap, D, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
+    check("int8k_decode_attention_forward_cache", st)
     return out

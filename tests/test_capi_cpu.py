@@ -64,3 +64,56 @@ def test_decode_split_plan(capi, BH, S, D):
     # the headline config fills 256 CUs many times over
     if (BH, S, D) == (1024, 8192, 128):
         assert BH * ns >= 4096
+
+
+def test_prefill_argument_validation(capi):
+    lib = capi.load()
+    f = lambda **kw: lib.int8k_attention_forward(  # noqa: E731
+        _fake(kw.get("Q", 0x10000)), _fake(0x20000), _fake(0x30000), _fake(kw.get("out", 0x40000)),
+        _fake(0x50000), _fake(0x60000), _fake(0x70000), kw.get("B", 1), 2, kw.get("S", 64),
+        kw.get("D", 128), 0, None)
+    assert f(Q=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(S=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(B=-1) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(D=96) == capi.INT8K_ERR_UNSUPPORTED
+    assert f(Q=0x10008) == capi.INT8K_ERR_MISALIGNED
+    assert f(out=0x40002) == capi.INT8K_ERR_MISALIGNED
+
+
+def test_mlp_argument_validation(capi):
+    lib = capi.load()
+
+    def f(n_sx=4, dm=64, dff=128, flags=0, ws=0x90000, ws_bytes=1 << 30, x=0x10000):
+        return lib.int8k_mlp_forward(_fake(x), _fake(0x20000), _fake(0x30000), _fake(0x40000),
+                                     _fake(0x50000), n_sx, _fake(0x60000), 1, _fake(0x70000), 1,
+                                     None, _fake(0x80000), 4, dm, dff, flags, _fake(ws),
+                                     ws_bytes, None)
+    assert f(x=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(n_sx=3) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(flags=8) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(dm=60) == capi.INT8K_ERR_UNSUPPORTED
+    assert f(x=0x10004) == capi.INT8K_ERR_MISALIGNED
+    need = capi.mlp_workspace_bytes(4, 64, 128, 0)
+    assert f(ws_bytes=need - 1) == capi.INT8K_ERR_WORKSPACE
+    assert capi.mlp_workspace_bytes(4, 64, 128, capi.MLP_WEIGHTS_PREPACKED) < need
+    assert lib.int8k_gemm_i8_i32(_fake(0x10000), _fake(0x20000), _fake(0x30000), 4, 4, 40,
+                                 None) == capi.INT8K_ERR_UNSUPPORTED
+
+
+def test_quant_argument_validation(capi):
+    lib = capi.load()
+    assert lib.int8k_quantize_per_token(_fake(0x10000), 7, _fake(0x20000), _fake(0x30000), 4,
+                                        64, None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert lib.int8k_quantize_per_token(_fake(0x10001), 0, _fake(0x20000), _fake(0x30000), 4,
+                                        64, None) == capi.INT8K_ERR_MISALIGNED
+    assert lib.int8k_quantize_fp16_to_int8(_fake(0x10000), _fake(0x20000), None, 16,
+                                           None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    # append past the capacity
+    assert lib.int8k_kv_cache_append(_fake(0x10000), _fake(0x20000), 0, _fake(0x30000),
+                                     _fake(0x40000), _fake(0x50000), _fake(0x60000), 2, 5, 96,
+                                     100, 64, None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    # decode over a cache shorter than the attended length
+    assert lib.int8k_decode_attention_forward_cache(
+        _fake(0x10000), _fake(0x20000), _fake(0x30000), _fake(0x40000), _fake(0x50000),
+        _fake(0x60000), _fake(0x70000), 4, 200, 100, 128, 0, _fake(0x80000), 1 << 30,
+        None) == capi.INT8K_ERR_INVALID_ARGUMENT

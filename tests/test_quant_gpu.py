@@ -1,0 +1,114 @@
+"""Quantizers and the INT8 KV cache against the CPU oracle (GPU tests).
+
+The quantizers are bit-exact by construction (exact absmax, correctly rounded
+fp32 division, round-half-even), so codes and scales must match the oracle
+exactly; the cache-backed decode must equal the contiguous decode bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import int8k_capi as capi
+import workloads
+from oracle import int8_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (7, 33), (1000, 128), (3, 5, 64), (64, 4096)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_quantize_per_token_bit_exact(ext, gpu, shape, dtype):
+    g = torch.Generator().manual_seed(sum(shape))
+    x = (torch.randn(shape, generator=g) * 3).to(dtype)
+    q, s = ext.quantize_per_token(x.to(gpu))
+    rq, rs = O.quantize_per_token(x.float().numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    np.testing.assert_array_equal(s.cpu().numpy(), rs)
+    assert q.shape == x.shape and tuple(s.shape) == shape[:-1]
+
+
+def test_quantize_per_token_kats(ext, gpu):
+    x = torch.zeros(4, 64, device=gpu)
+    x[1] = 2.0                                        # constant row -> code 127
+    x[2, ::2], x[2, 1::2] = 0.5, -0.5
+    x[3] = torch.linspace(-127, 127, 64, device=gpu)  # scale 1: codes are rint(x)
+    q, s = ext.quantize_per_token(x)
+    assert int(q[0].abs().max()) == 0 and float(s[0]) == np.float32(np.float32(1e-8) / 127)
+    assert int(q[1].min()) == int(q[1].max()) == 127
+    assert set(q[2].tolist()) == {127, -127}
+    np.testing.assert_array_equal(q[3].cpu().numpy(), np.rint(x[3].cpu().numpy()).astype(np.int8))
+    # boundary dataset (validation/generate_test_data.py:113-122): codes +-125..127
+    g = torch.Generator().manual_seed(3)
+    sign = torch.randint(0, 2, (32, 128), generator=g).float() * 2 - 1
+    xb = sign * 4.0 * (0.985 + 0.015 * torch.rand(32, 128, generator=g))
+    q, _ = ext.quantize_per_token(xb.to(gpu))
+    assert set(q.abs().unique().tolist()) <= {125, 126, 127}
+
+
+def test_quantize_per_token_matches_reference_formula_on_cpu(ext, gpu):
+    # The reference quantizer's torch formula evaluated on the CPU (true fp32
+    # division) is reproduced bit for bit.  (On the GPU torch turns the
+    # division by the scalar 127 into a reciprocal multiply, so its scales may
+    # differ from the formula in the last ulp.)
+    x = torch.randn(512, 128, generator=torch.Generator().manual_seed(1))
+    q, s = ext.quantize_per_token(x.to(gpu))
+    rq, rs = workloads.quantize_per_token(x)
+    assert torch.equal(q.cpu(), rq) and torch.equal(s.cpu(), rs)
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+def test_quant_utils_per_tensor(ext, gpu, n):
+    x = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 5).half()
+    q, s = ext.quantize_fp16_to_int8(x.to(gpu))
+    rq, rs = O.quantize_fp16_per_tensor(x.numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    assert float(s) == float(rs)
+    y = ext.dequantize_int8_to_fp16(q, float(s))
+    np.testing.assert_array_equal(y.cpu().numpy(), O.dequantize_int8_to_fp16(rq, rs))
+
+
+def test_quant_utils_zero_input(ext, gpu):
+    q, s = ext.quantize_fp16_to_int8(torch.zeros(4096, dtype=torch.float16, device=gpu))
+    assert int(q.abs().max()) == 0                     # not -128 as the reference kernel gives
+    assert float(s) == float(np.float32(np.float32(1e-8) / np.float32(127)))
+
+
+def test_kv_cache_append_and_decode(ext, gpu):
+    B, H, D, cap = 2, 4, 128, 640
+    g = torch.Generator().manual_seed(11)
+    k_all = torch.randn(B, H, 300, D, generator=g).half().to(gpu)
+    v_all = torch.randn(B, H, 300, D, generator=g).half().to(gpu)
+    K = torch.zeros(B, H, cap, D, dtype=torch.int8, device=gpu)
+    V = torch.zeros_like(K)
+    sK = torch.zeros(B, H, cap, device=gpu)
+    sV = torch.zeros_like(sK)
+    ext.kv_cache_append(k_all[:, :, :257], v_all[:, :, :257], K, V, sK, sV, 0)  # prefill
+    for p in range(257, 300):                                                   # decode steps
+        ext.kv_cache_append(k_all[:, :, p:p + 1], v_all[:, :, p:p + 1], K, V, sK, sV, p)
+    kq, ks = workloads.quantize_per_token(k_all.cpu())
+    vq, vs = workloads.quantize_per_token(v_all.cpu())
+    assert torch.equal(K[:, :, :300].cpu(), kq) and torch.equal(sK[:, :, :300].cpu(), ks)
+    assert torch.equal(V[:, :, :300].cpu(), vq) and torch.equal(sV[:, :, :300].cpu(), vs)
+    kq, ks, vq, vs = (t.to(gpu) for t in (kq, ks, vq, vs))
+    assert int(K[:, :, 300:].abs().max()) == 0            # untouched past the append
+    q, sq = workloads.quantize_per_token(torch.randn(B, H, D, generator=g).to(gpu))
+    a = ext.int8_decode_attention_forward_cache(q, K, V, sq, sK, sV, 300)
+    b = ext.int8_decode_attention_forward(q, kq.contiguous(), vq.contiguous(), sq, ks, vs)
+    assert torch.equal(a, b)
+    with pytest.raises(RuntimeError, match="capacity"):
+        ext.kv_cache_append(k_all[:, :, :1], v_all[:, :, :1], K, V, sK, sV, cap)
+
+
+def test_kv_cache_capi(gpu):
+    B, H, D, cap = 1, 2, 64, 100
+    k = torch.randn(B, H, 10, D, device=gpu)
+    v = torch.randn(B, H, 10, D, device=gpu)
+    K = torch.zeros(B, H, cap, D, dtype=torch.int8, device=gpu)
+    V = torch.zeros_like(K)
+    sK = torch.zeros(B, H, cap, device=gpu)
+    sV = torch.zeros_like(sK)
+    capi.kv_cache_append(k, v, K, V, sK, sV, 90)
+    torch.cuda.synchronize()
+    kq, ks = O.quantize_per_token(k.cpu().numpy())
+    np.testing.assert_array_equal(K[:, :, 90:].cpu().numpy(), kq)
+    np.testing.assert_array_equal(sK[:, :, 90:].cpu().numpy(), ks)
