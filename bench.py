@@ -210,12 +210,150 @@ def bench_decode(args):
     return res
 
 
+INT8_PEAK_TOPS = 5000.0
+FP16_PEAK_TFLOPS = 2500.0
+BLENDED_PEAK = 1.0 / (0.5 / INT8_PEAK_TOPS + 0.5 / FP16_PEAK_TFLOPS)  # i8 QK^T + fp16 PV
+
+
+def bench_mlp(args):
+    """T=4096, 4096 -> 16384 -> 4096, per-token x, per-channel W."""
+    import numpy as np
+    import torch
+
+    import int8k_capi as capi
+    import workloads
+    from oracle import int8_oracle, oracle_c
+
+    T, dm, dff = 4096, 4096, 16384
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] generating MLP inputs T={T} {dm}->{dff}->{dm}")
+    c = workloads.mlp_case(T, dm, dff, seed=args.seed, device=dev)
+    x = c["x"].reshape(T, dm)
+    W1T, W2T = capi.transpose_int8_weights(c["W1"], c["W2"])
+    out = torch.empty(T, dm, dtype=torch.int8, device=dev)
+    osc = torch.empty(T, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    ops = 4 * T * dm * dff
+    res_lines = {}
+    for name, flags, w1, w2 in (("prepacked", capi.MLP_WEIGHTS_PREPACKED, W1T, W2T),
+                                ("unpacked", 0, c["W1"], c["W2"])):
+        ws = torch.empty(capi.mlp_workspace_bytes(T, dm, dff, flags), dtype=torch.uint8,
+                         device=dev)
+
+        def step():
+            capi.mlp_forward(x, w1, w2, c["sx"], c["sW1"], c["sW2"], flags=flags, out=out,
+                             out_scale=osc, workspace=ws)
+
+        ms = time_steps(step, args.steps, args.warmup, stream)
+        res_lines[name] = ms
+        log(f"[bench] MLP {name}: {ms * 1e3:.1f} us  {ops / (ms * 1e-3) / 1e12:.1f} TOPS")
+        del ws
+    rows = np.arange(0, T, T // 8)
+    ref, rsc = int8_oracle.mlp_forward(x[rows].cpu().numpy(), c["W1"].cpu().numpy(),
+                                       c["W2"].cpu().numpy(), c["sx"][rows].cpu().numpy(),
+                                       c["sW1"].cpu().numpy(), c["sW2"].cpu().numpy(),
+                                       gemm=oracle_c.gemm_i8_i32)
+    diff = np.abs(out[rows].cpu().numpy().astype(np.int32) - ref.astype(np.int32)).max()
+    log(f"[bench] parity sample ({len(rows)} rows): max |int8 diff| = {diff}")
+    if diff > 1:
+        raise SystemExit("MLP output does not match the oracle within 1 LSB")
+    ms = res_lines["prepacked"]
+    tops = ops / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "fused INT8 MLP TOPS (% dense INT8 MFMA peak), T=4096 4096->16384->4096",
+        "value": round(tops, 1), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) x, N(0,0.02) W, per-token/per-channel int8)",
+        "config": {"workload": "int8 MLP T=4096 d_model=4096 d_ff=16384 GELU, prepacked weights",
+                   "unpacked_ms_per_step": round(res_lines["unpacked"], 5)},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "traffic": measured_traffic("mlp_t4096_d4096_f16384"),
+                     "kernel": "whole MLP step (2 GEMMs + requant kernels)"},
+    }
+    if not args.no_cpu_baseline:
+        threads = oracle_c.max_threads()
+        n = 4
+        t0 = time.perf_counter()
+        int8_oracle.mlp_forward(x[:n].cpu().numpy(), c["W1"].cpu().numpy(), c["W2"].cpu().numpy(),
+                                c["sx"][:n].cpu().numpy(), c["sW1"].cpu().numpy(),
+                                c["sW2"].cpu().numpy(), gemm=oracle_c.gemm_i8_i32)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": 4 * n * dm * dff / dt / 1e12, "unit": "TOPS",
+                               "cores": threads, "kind": "port",
+                               "sample": f"oracle MLP (C int8 GEMMs, numpy epilogue) on {n} of "
+                                         f"{T} tokens; {dt:.1f} s"}
+    return res
+
+
+def bench_prefill(args):
+    """B=4 H=32 S=4096 D=128, causal."""
+    import numpy as np
+    import torch
+
+    import int8k_capi as capi
+    import workloads
+    from oracle import oracle_c
+
+    B, H, S, D = 4, 32, 4096, 128
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] generating prefill inputs B{B} H{H} S{S} D{D}")
+    c = workloads.prefill_case(B, H, S, D, seed=args.seed, device=dev)
+    out = torch.empty(B, H, S, D, dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    res_ms = {}
+    for causal in (True, False):
+        def step():
+            capi.attention_forward(c["Qi"], c["Ki"], c["Vi"], c["sQ"], c["sK"], c["sV"],
+                                   causal=causal, out=out)
+        res_ms[causal] = time_steps(step, args.steps, args.warmup, stream)
+        ops = 2 * B * H * D * S * (S + 1) if causal else 4 * B * H * S * S * D
+        log(f"[bench] prefill causal={causal}: {res_ms[causal] * 1e3:.1f} us  "
+            f"{ops / (res_ms[causal] * 1e-3) / 1e12:.1f} TOPS")
+    ms = res_ms[True]
+    ops = 2 * B * H * D * S * (S + 1)
+    tops = ops / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "INT8 causal prefill attention TOPS, B=4 H=32 S=4096 D=128",
+        "value": round(tops, 1), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1), per-token int8)",
+        "config": {"workload": "int8 causal prefill attention B=4 H=32 S=4096 D=128",
+                   "noncausal_ms_per_step": round(res_ms[False], 5),
+                   "blended_peak_TOPS": round(BLENDED_PEAK, 1)},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "frac_of_blended_i8_f16": round(tops / BLENDED_PEAK, 4), "traffic": None,
+                     "kernel": "prefill_kernel<128, causal>"},
+    }
+    if not args.no_cpu_baseline:
+        threads = oracle_c.max_threads()
+        Sb = 1024
+        q = c["Qi"][0, :2, :Sb].cpu().numpy()
+        k = c["Ki"][0, :2, :Sb].cpu().numpy()
+        v = c["Vi"][0, :2, :Sb].cpu().numpy()
+        sq, sk, sv = (c[n][0, :2, :Sb].cpu().numpy() for n in ("sQ", "sK", "sV"))
+        t0 = time.perf_counter()
+        oracle_c.prefill_attention(q, k, v, sq, sk, sv, causal=True, threads=threads)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": 2 * 2 * D * Sb * (Sb + 1) / dt / 1e12, "unit": "TOPS",
+                               "cores": threads, "kind": "port",
+                               "sample": f"C oracle causal attention (float64) on 2 heads x "
+                                         f"{Sb} tokens; {dt:.2f} s"}
+    _ = np
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "prefill"])
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--head-dim", type=int, default=128)
@@ -230,7 +368,12 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(decode shards over (b,h) with no exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    res = bench_decode(args)
+    if args.workload == "mlp":
+        res = bench_mlp(args)
+    elif args.workload == "prefill":
+        res = bench_prefill(args)
+    else:
+        res = bench_decode(args)
     print(json.dumps(res), flush=True)
 
 
