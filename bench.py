@@ -77,9 +77,35 @@ def calibrate(dev):
     mfma_tops = blocks * 4 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
     del buf
     torch.cuda.empty_cache()
+    sustained = mfma_sustained(L, dev)
     return {"hbm_stream_read_TBps": round(read_tbs, 3), "hbm_copy_rw_TBps": round(copy_tbs, 3),
-            "mfma_i8_16x16x64_TOPS": round(mfma_tops, 1),
+            "mfma_i8_16x16x64_TOPS": round(mfma_tops, 1), **sustained,
             "copy_kernel_bytes": {"read": half, "write": half}}
+
+
+def mfma_sustained(L, dev, steps=10):
+    """Back-to-back v_mfma_i32_32x32x32_i8 (one wave per SIMD, ~0.3 ms launches) with
+    operands drawn from uniform random int8 and from zeros: the part's sustained clock,
+    and so its MFMA rate, depends on the operand bits toggled."""
+    import ctypes
+
+    import torch
+
+    stream = torch.cuda.current_stream(dev)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    blocks, iters = 256, 1000
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    out = {}
+    for name, src in (("random", torch.randint(-128, 128, (blocks * 8192,), dtype=torch.int8,
+                                               device=dev, generator=g)),
+                      ("zero", torch.zeros(blocks * 8192, dtype=torch.int8, device=dev))):
+        ms = time_steps(lambda: L.int8k_calib_mfma_i8_32_src(
+            ctypes.c_void_p(src.data_ptr()), blocks, iters, ctypes.c_void_p(sink.data_ptr()), st),
+            steps, 2, stream)
+        out[f"mfma_i8_32x32x32_sustained_{name}_TOPS"] = round(
+            blocks * 4 * iters * 16 * 65536 / (ms * 1e-3) / 1e12, 1)
+    return out
 
 
 def cpu_baseline_decode(case, B, H, D, S, budget_s=12.0):
@@ -273,6 +299,10 @@ def bench_mlp(args):
                      "traffic": measured_traffic("mlp_t4096_d4096_f16384"),
                      "kernel": "whole MLP step (2 GEMMs + requant kernels)"},
     }
+    if not args.no_calibrate:
+        import ctypes
+        res["ceilings"] = mfma_sustained(ctypes.CDLL(os.path.join(PKG_DIR, "libint8k_calib.so")),
+                                         dev)
     if not args.no_cpu_baseline:
         threads = oracle_c.max_threads()
         n = 4
@@ -348,12 +378,59 @@ def bench_prefill(args):
     return res
 
 
+def bench_gemm(args):
+    """The MLP's GEMM1 shape alone (4096 x 16384 x 4096, int32 out): our gemm core on uniform
+    random and on all-zero operands, and hipBLASLt (torch._int_mm) on the random operands.
+    Shows how far the sustained MFMA rate depends on the operand data on this part."""
+    import ctypes
+
+    import torch
+
+    import int8k_capi as capi
+
+    M, N, K = 4096, 16384, 4096
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    A = torch.randint(-128, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+    Bt = torch.randint(-128, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    C = torch.empty(M, N, dtype=torch.int32, device=dev)
+    ops = 2 * M * N * K
+    ms_rand = time_steps(lambda: capi.gemm_i8_i32(A, Bt, out=C), args.steps, args.warmup, stream)
+    ref = A[:64].double().cpu() @ Bt.double().cpu().t()
+    if not torch.equal(C[:64].cpu().double(), ref):
+        raise SystemExit("gemm_i8_i32 does not match the exact int32 product")
+    ms_lib = time_steps(lambda: torch._int_mm(A, Bt.t()), args.steps, args.warmup, stream)
+    A.zero_()
+    Bt.zero_()
+    ms_zero = time_steps(lambda: capi.gemm_i8_i32(A, Bt, out=C), args.steps, args.warmup, stream)
+    tops = ops / (ms_rand * 1e-3) / 1e12
+    for name, ms in (("random", ms_rand), ("zero", ms_zero), ("hipblaslt random", ms_lib)):
+        log(f"[bench] gemm {name}: {ms * 1e3:.1f} us  {ops / (ms * 1e-3) / 1e12:.1f} TOPS")
+    L = ctypes.CDLL(os.path.join(PKG_DIR, "libint8k_calib.so"))
+    return {
+        "metric": "INT8 GEMM TOPS, 4096x16384x4096 (the MLP's GEMM1 shape), int32 out",
+        "value": round(tops, 1), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_rand, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic uniform random int8 (and all-zero for the comparison)",
+        "config": {"workload": "int8 GEMM M=4096 N=16384 K=4096",
+                   "zero_operands_TOPS": round(ops / (ms_zero * 1e-3) / 1e12, 1),
+                   "hipblaslt_int_mm_random_TOPS": round(ops / (ms_lib * 1e-3) / 1e12, 1)},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "traffic": None, "kernel": "gemm_i8_kernel<0>"},
+        "ceilings": mfma_sustained(L, dev),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "prefill"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "prefill", "gemm"])
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--head-dim", type=int, default=128)
@@ -372,6 +449,8 @@ def main():
         res = bench_mlp(args)
     elif args.workload == "prefill":
         res = bench_prefill(args)
+    elif args.workload == "gemm":
+        res = bench_gemm(args)
     else:
         res = bench_decode(args)
     print(json.dumps(res), flush=True)

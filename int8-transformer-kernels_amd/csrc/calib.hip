@@ -9,6 +9,11 @@
 //   int8k_calib_mfma_i8     : back-to-back v_mfma_i32_16x16x64_i8 on
 //       independent accumulators, no memory traffic, giving the dense INT8
 //       MFMA ceiling as 2*16*16*64 ops per instruction.
+//   int8k_calib_mfma_i8_32_src : 16 independent v_mfma_i32_32x32x32_i8
+//       accumulators per wave with operands loaded from a caller buffer, so
+//       the sustained ceiling can be measured with the operand values a GEMM
+//       sees (the MFMA rate this part sustains depends on the data: its power
+//       draw sets the clock).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -94,6 +99,31 @@ __global__ __launch_bounds__(256) void calib_mfma_i8_32_kernel(int iters, int* _
     sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s[0] ^ s[5] ^ s[10] ^ s[15];
 }
 
+// One wave per SIMD at 256 blocks; operands a[4], b[4] per lane from src (8 KiB per block).
+__global__ __launch_bounds__(256) void calib_mfma_i8_32_src_kernel(const v4i* __restrict__ src,
+                                                                   int iters,
+                                                                   int* __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v4i a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = src[(blockIdx.x * 8 + i) * 64 + lane];
+        b[i] = src[(blockIdx.x * 8 + 4 + i) * 64 + lane];
+    }
+    v16i_t c[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c[i] = v16i_t{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i & 3], b[i >> 2], c[i], 0, 0, 0);
+    }
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s ^= c[i][0] ^ c[i][7] ^ c[i][15];
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 extern "C" int int8k_calib_stream_read(const void* buf, size_t bytes, int* sink, int blocks,
                                        void* stream) {
     calib_stream_read_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
@@ -120,6 +150,14 @@ extern "C" int int8k_calib_copy(const void* src, void* dst, size_t bytes, int bl
 // ops per launch = blocks * 4 waves * iters * 4 MFMAs * 65536
 extern "C" int int8k_calib_mfma_i8_32(int blocks, int iters, int* sink, void* stream) {
     calib_mfma_i8_32_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(iters, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// ops per launch = blocks * 4 waves * iters * 16 MFMAs * 65536; src holds blocks * 8 KiB
+extern "C" int int8k_calib_mfma_i8_32_src(const void* src, int blocks, int iters, int* sink,
+                                          void* stream) {
+    calib_mfma_i8_32_src_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>((const v4i*)src, iters,
+                                                                         sink);
     return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 
