@@ -92,4 +92,31 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
     return __half_as_ushort(__float2half_rn(x));
 }
 
+// Raw buffer resource over [base, base + bytes): loads at offsets past the end
+// return zero, so tiles that overhang a matrix need no clamped addresses.  The
+// arguments must be the same for the whole wave (they go to scalar registers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer(const void* base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint64_t ub =
+        (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)))
+         << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(ub), 0,
+                                             __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// Byte J of two dwords whose bytes were XORed with 0x80 (int8 -> biased
+// uint8), as a packed pair of fp16 integers {lo: byte J of w0, hi: of w1}.
+// 0x6400 | u is the fp16 value 1024 + u (exact for u < 1024), so one
+// v_perm_b32, one OR and one v_pk_add_f16 convert two int8 values.
+template <int J>
+__device__ __forceinline__ uint32_t biased_bytes_to_f16x2(uint32_t w0x, uint32_t w1x) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    constexpr uint32_t sel = J | (0x0Cu << 8) | ((4u + J) << 16) | (0x0Cu << 24);
+    const uint32_t u = __builtin_amdgcn_perm(w1x, w0x, sel) | 0x64006400u;
+    h2 v = __builtin_bit_cast(h2, u);
+    v = v + h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 }  // namespace int8k

@@ -37,6 +37,10 @@ constexpr int kQ = 128;        // queries per block
 constexpr int kKV = 64;        // keys per tile
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
+// How far (log2 units) a tile's max may exceed the running reference max before
+// O is rescaled: p <= 2^4 on the fast path, so p * sV stays finite in fp16 for
+// any sV below 4094 (V from fp16 data has sV <= 65504/127 = 516).
+constexpr float kRescaleSlack = 4.0f;
 
 // LDS position of key kk (0..63) of a tile inside a V^T row: keys
 // 16t + 8a + 4h + c are stored at 16t + 8h + 4a + c, so the 8 keys that lane
@@ -57,6 +61,29 @@ struct Stage {
     static constexpr int kVItems = kKV * D / 16 / kThreads;        // 4x4 V blocks per thread
 };
 
+// Buffer resources over one (b,h)'s K, V and scales.  Rows at or past S read
+// as zero, so the tile loads need no clamping; masked keys never reach the
+// output.
+struct TileSrc {
+    __amdgpu_buffer_rsrc_t k, v, s;
+    uint32_t voff_k, voff_v, voff_s;
+};
+
+template <int D>
+__device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t* Vbh,
+                                                 const float* sKbh, const float* sVbh, int S) {
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    TileSrc src;
+    src.k = make_buffer(Kbh, (uint32_t)S * D);
+    src.v = make_buffer(Vbh, (uint32_t)S * D);
+    src.s = make_buffer(wave == 0 ? sKbh : sVbh, (uint32_t)S * 4);  // waves 0 and 1 load scales
+    src.voff_k = (t / (D / 16)) * D + (t % (D / 16)) * 16;
+    src.voff_v = 4 * (t / (D / 4)) * D + 4 * (t % (D / 4));
+    src.voff_s = (t & (kKV - 1)) * 4;
+    return src;
+}
+
 // Registers holding the next tile while the current one is computed.
 template <int D>
 struct Prefetch {
@@ -65,36 +92,30 @@ struct Prefetch {
     float sc;  // threads 0..63: sK of key tid; 64..127: sV of key tid-64
 };
 
+// Thread t loads 16-byte K chunk t + 256 n (row (t + 256 n) / (D/16)) and the
+// 4x4 int8 V block t + 256 n (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3); in
+// both cases consecutive n are 4096 bytes apart.
 template <int D>
-__device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const int8_t* __restrict__ Kbh,
-                                              const int8_t* __restrict__ Vbh,
-                                              const float* __restrict__ sKbh,
-                                              const float* __restrict__ sVbh, int k0, int S) {
-    const int t = threadIdx.x;
+__device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& src, int k0) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
-        const int c = t + n * kThreads;
-        const int row = c / (D / 16), col = (c % (D / 16)) * 16;
-        pf.k[n] = *reinterpret_cast<const int4*>(Kbh + (size_t)min(k0 + row, S - 1) * D + col);
+        const v4u w = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.voff_k, k0 * D + n * 4096, 0);
+        pf.k[n] = make_int4((int)w.x, (int)w.y, (int)w.z, (int)w.w);
     }
 #pragma unroll
-    for (int n = 0; n < Stage<D>::kVItems; ++n) {
-        const int it = t + n * kThreads;
-        const int kg = it / (D / 4), dg = it % (D / 4);
+    for (int n = 0; n < Stage<D>::kVItems; ++n)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            pf.v[n][i] = *reinterpret_cast<const uint32_t*>(
-                Vbh + (size_t)min(k0 + 4 * kg + i, S - 1) * D + 4 * dg);
-    }
-    if (t < 2 * kKV) {
-        const int key = min(k0 + (t & (kKV - 1)), S - 1);
-        pf.sc = t < kKV ? sKbh[key] : sVbh[key];
-    }
+            pf.v[n][i] = __builtin_amdgcn_raw_buffer_load_b32(src.v, src.voff_v,
+                                                              k0 * D + n * 4096 + i * D, 0);
+    if (threadIdx.x < 2 * kKV)
+        pf.sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.s, src.voff_s,
+                                                                               k0 * 4, 0));
 }
 
 template <int D>
 __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
-    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
     const int t = threadIdx.x;
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
@@ -108,14 +129,18 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
         const int it = t + n * kThreads;
         const int kg = it / (D / 4), dg = it % (D / 4);
         const int p0 = vt_pos(4 * kg);
+        uint32_t x[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            _Float16 h[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                h[i] = (_Float16)(float)(int8_t)((pf.v[n][i] >> (8 * j)) & 0xff);
-            *reinterpret_cast<v4h*>(vt + (4 * dg + j) * kVtStride + p0) = v4h{h[0], h[1], h[2], h[3]};
-        }
+        for (int i = 0; i < 4; ++i) x[i] = pf.v[n][i] ^ 0x80808080u;
+        // dim 4 dg + j of keys 4 kg .. 4 kg + 3 -> 4 consecutive fp16 of V^T row 4 dg + j
+        *reinterpret_cast<uint2*>(vt + (4 * dg + 0) * kVtStride + p0) =
+            make_uint2(biased_bytes_to_f16x2<0>(x[0], x[1]), biased_bytes_to_f16x2<0>(x[2], x[3]));
+        *reinterpret_cast<uint2*>(vt + (4 * dg + 1) * kVtStride + p0) =
+            make_uint2(biased_bytes_to_f16x2<1>(x[0], x[1]), biased_bytes_to_f16x2<1>(x[2], x[3]));
+        *reinterpret_cast<uint2*>(vt + (4 * dg + 2) * kVtStride + p0) =
+            make_uint2(biased_bytes_to_f16x2<2>(x[0], x[1]), biased_bytes_to_f16x2<2>(x[2], x[3]));
+        *reinterpret_cast<uint2*>(vt + (4 * dg + 3) * kVtStride + p0) =
+            make_uint2(biased_bytes_to_f16x2<3>(x[0], x[1]), biased_bytes_to_f16x2<3>(x[2], x[3]));
     }
     if (t < 2 * kKV)
         reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
@@ -156,6 +181,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
     for (int s = 0; s < NS; ++s)
         qf[s] = *reinterpret_cast<const v4i*>(Qbh + (size_t)min(q, S - 1) * D + 32 * s + 16 * h);
     const float qscale = qok ? sQ[base + q] * qk_scale_log2 : 0.f;
+    const bool qpos = __ballot(!(qscale >= 0.f)) == 0;  // wave-uniform
 
     v16f o[NS];
 #pragma unroll
@@ -169,39 +195,126 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
     const int n_kv = (kv_end + kKV - 1) / kKV;
     const int q_wave_last = min(qw0 + 31, S - 1);
 
-    // Pipeline: tile kt is computed from LDS stage kt&1.  Two register sets
-    // (pa, pb) hold the next two tiles, so each tile's global loads have two
-    // tile-steps to land before they are committed to LDS at the end of the
-    // step that precedes their use; the step's only barrier follows the commit.
-    Prefetch<D> pa, pb;
-    prefetch_tile<D>(pa, Kbh, Vbh, sKbh, sVbh, 0, S);
-    commit_tile<D>(pa, smem);
-    if (n_kv > 1) prefetch_tile<D>(pa, Kbh, Vbh, sKbh, sVbh, kKV, S);
-    if (n_kv > 2) prefetch_tile<D>(pb, Kbh, Vbh, sKbh, sVbh, 2 * kKV, S);
+    // Pipeline: tile kt is computed from LDS stage kt&1.  The register set pf
+    // holds tile kt+1 while tile kt is computed; at the end of the step it is
+    // written to the other stage, refilled with tile kt+2, and the step's one
+    // barrier follows.
+    const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S);
+    Prefetch<D> pf;
+    prefetch_tile<D>(pf, src, 0);
+    commit_tile<D>(pf, smem);
+    if (n_kv > 1) prefetch_tile<D>(pf, src, kKV);
     __syncthreads();
-    auto step = [&](int kt, Prefetch<D>& cur_pf) {
-        const int k0 = kt * kKV;
-        const char* st = smem + (kt & 1) * St::kBytes;
-        const _Float16* vt = reinterpret_cast<const _Float16*>(st + St::kKBytes);
-        const float* sk_l = reinterpret_cast<const float*>(st + St::kKBytes + St::kVtBytes);
-        const float* sv_l = sk_l + kKV;
-        if (!(CAUSAL && k0 > q_wave_last)) {  // skip tiles wholly masked for this wave
-            // S^T = K . Q^T for the two 32-key halves of the tile
-            v16i sacc[2];
+    auto advance = [&](int kt) {
+        if (kt + 1 < n_kv) {
+            commit_tile<D>(pf, smem + ((kt + 1) & 1) * St::kBytes);
+            if (kt + 2 < n_kv) prefetch_tile<D>(pf, src, (kt + 2) * kKV);
+        }
+        // tile kt+1 is in LDS and every wave is done reading stage kt&1
+        __syncthreads();
+    };
+    auto stage_of = [&](int kt) { return smem + (kt & 1) * St::kBytes; };
+    // S^T = K . Q^T for the two 32-key halves of tile kt
+    auto qk = [&](int kt, v16i (&sacc)[2]) {
+        const char* st = stage_of(kt);
 #pragma unroll
-            for (int T = 0; T < 2; ++T) {
+        for (int T = 0; T < 2; ++T) {
+            v4i kf[NS];
+            const char* krow = st + (32 * T + (lane & 31)) * St::kKStride + 16 * h;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[T][r] = 0;
-                const char* krow = st + (32 * T + (lane & 31)) * St::kKStride + 16 * h;
+            for (int s = 0; s < NS; ++s) kf[s] = *reinterpret_cast<const v4i*>(krow + 32 * s);
 #pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    const v4i kf = *reinterpret_cast<const v4i*>(krow + 32 * s);
-                    sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[s], sacc[T], 0, 0, 0);
-                }
+            for (int r = 0; r < 16; ++r) sacc[T][r] = 0;
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+                sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[s], qf[s], sacc[T], 0, 0, 0);
+        }
+    };
+    // O^T += V^T . P'^T
+    auto pv = [&](int kt, const v8h (&pfr)[4]) {
+        const _Float16* vt = reinterpret_cast<const _Float16*>(stage_of(kt) + St::kKBytes);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const _Float16* row = vt + (32 * t + (lane & 31)) * kVtStride + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const v8h vf = *reinterpret_cast<const v8h*>(row + 16 * ks);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pfr[ks], o[t], 0, 0, 0);
             }
-            // scores (log2 domain) of this lane's 32 keys:
-            // key = k0 + 32T + 8g + 4h + c  <->  sacc[T][4g + c]
-            const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
+        }
+    };
+    auto sk_of = [&](int kt) {
+        return reinterpret_cast<const float*>(stage_of(kt) + St::kKBytes + St::kVtBytes);
+    };
+    // A wave computes tile kt unless the causal mask hides all of it from the wave's queries.
+    auto computes = [&](int kt) { return !(CAUSAL && kt * kKV > q_wave_last); };
+
+    // Scores of this lane's 32 keys: key = k0 + 32T + 8g + 4h + c <-> sacc[T][4g + c];
+    // P'^T = p * sV (fp16): slice t = registers [8(t%2), 8(t%2)+8) of half t/2.
+    //
+    // The running max m is a reference, not necessarily the exact running max: a
+    // tile takes the fast path when it has no masked key, every lane's qscale is
+    // >= 0 and no lane's tile max exceeds m by more than kRescaleSlack (log2
+    // units).  Then p = 2^(u*qscale - m) <= 2^kRescaleSlack, O is only updated by
+    // the PV MFMAs (in place), and the rescale is skipped.  Every other tile
+    // (first tile, masked edge and diagonal tiles, a large max increase) takes the
+    // slow path, which sets m to the exact running max and rescales O and l.
+    // The fast path runs as an inner loop that the slow path leaves and
+    // re-enters, so O has no conditional update inside it.
+    int kt = 0;
+    while (kt < n_kv) {
+        v16i sacc[2];
+        bool slow = false;
+        for (; kt < n_kv; ++kt) {
+            if (computes(kt)) {
+                qk(kt, sacc);
+                const int k0 = kt * kKV;
+                const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
+                if (!(full && qpos)) { slow = true; break; }
+                const float* sk_l = sk_of(kt);
+                float u[2][16];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
+                        const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            u[T][4 * g + c] = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
+                            mx = fmaxf(mx, u[T][4 * g + c]);
+                        }
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                if (__ballot(!(mx * qscale <= m + kRescaleSlack))) { slow = true; break; }
+                const float neg_m = -m;
+                const float* sv_l = sk_l + kKV;
+                v8h pfr[4];
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 svv = *reinterpret_cast<const float4*>(sv_l + 32 * T + 8 * g + 4 * h);
+                        const float svk[4] = {svv.x, svv.y, svv.z, svv.w};
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const float p = fast_exp2(fmaf(u[T][4 * g + c], qscale, neg_m));
+                            lsum += p;
+                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
+                        }
+                    }
+                pv(kt, pfr);
+            }
+            advance(kt);
+        }
+        if (!slow) break;
+        // Slow path for tile kt (its S^T is in sacc): s = acc * qscale * sK with masked
+        // keys at -inf, exact running max, rescale of O and l.
+        {
+            const int k0 = kt * kKV;
+            const float* sk_l = sk_of(kt);
+            const float* sv_l = sk_l + kKV;
             float sc[2][16];
             float mx = -INFINITY;
 #pragma unroll
@@ -213,10 +326,8 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
-                        if (!full) {
-                            const int key = k0 + 32 * T + 8 * g + 4 * h + c;
-                            if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
-                        }
+                        const int key = k0 + 32 * T + 8 * g + 4 * h + c;
+                        if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
                         sc[T][4 * g + c] = v;
                         mx = fmaxf(mx, v);
                     }
@@ -224,18 +335,13 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float m_new = fmaxf(m, mx);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            // rescale only when some lane's running max moved (rare after the first tiles)
-            if (__ballot(m_new != m)) {
-                const float corr = fast_exp2(m - m_use);
-                lsum *= corr;
+            const float corr = fast_exp2(m - m_use);
+            lsum *= corr;
 #pragma unroll
-                for (int t = 0; t < NS; ++t)
+            for (int t = 0; t < NS; ++t)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-            }
+                for (int r = 0; r < 16; ++r) o[t][r] *= corr;
             m = m_new;
-
-            // P'^T = p * sV (fp16): slice t = registers [8(t%2), 8(t%2)+8) of half t/2
             v8h pfr[4];
 #pragma unroll
             for (int T = 0; T < 2; ++T)
@@ -250,28 +356,10 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
                         pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
                     }
                 }
-
-            // O^T += V^T . P'^T
-#pragma unroll
-            for (int t = 0; t < NS; ++t) {
-                const _Float16* row = vt + (32 * t + (lane & 31)) * kVtStride + 8 * h;
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const v8h vf = *reinterpret_cast<const v8h*>(row + 16 * ks);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pfr[ks], o[t], 0, 0, 0);
-                }
-            }
+            pv(kt, pfr);
         }
-        if (kt + 1 < n_kv) {
-            commit_tile<D>(cur_pf, smem + ((kt + 1) & 1) * St::kBytes);
-            if (kt + 3 < n_kv) prefetch_tile<D>(cur_pf, Kbh, Vbh, sKbh, sVbh, k0 + 3 * kKV, S);
-        }
-        // tile kt+1 is in LDS and every wave is done reading stage kt&1
-        __syncthreads();
-    };
-    for (int kt = 0; kt < n_kv; kt += 2) {
-        step(kt, pa);
-        if (kt + 1 < n_kv) step(kt + 1, pb);
+        advance(kt);
+        ++kt;
     }
 
     const float L = lsum + __shfl_xor(lsum, 32);
