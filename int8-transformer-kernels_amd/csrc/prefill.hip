@@ -50,6 +50,17 @@ __device__ __forceinline__ int vt_pos(int kk) {
     return 16 * t + 8 * h + 4 * a + c;
 }
 
+// Work item it of a V tile is the 4x4 block of keys 4 kg .. 4 kg + 3 and dims
+// 4 dg .. 4 dg + 3.  Key groups run fastest, so the 16 lanes that write one
+// V^T row (8 bytes each) fill it contiguously; the four 16-lane groups of a
+// wave take dim groups +0, +2, +1, +3, so the two groups that share an LDS
+// cycle write rows 8 apart (288 words: the other half of 64 banks).
+__device__ __forceinline__ int v_key_group(int it) { return it & 15; }
+__device__ __forceinline__ int v_dim_group(int it) {
+    const int g = (it >> 4) & 3;
+    return 4 * (it >> 6) + ((g & 1) << 1 | (g >> 1));
+}
+
 // One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16), scales.
 template <int D>
 struct Stage {
@@ -79,7 +90,7 @@ __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t
     src.v = make_buffer(Vbh, (uint32_t)S * D);
     src.s = make_buffer(wave == 0 ? sKbh : sVbh, (uint32_t)S * 4);  // waves 0 and 1 load scales
     src.voff_k = (t / (D / 16)) * D + (t % (D / 16)) * 16;
-    src.voff_v = 4 * (t / (D / 4)) * D + 4 * (t % (D / 4));
+    src.voff_v = 4 * v_key_group(t) * D + 4 * v_dim_group(t);
     src.voff_s = (t & (kKV - 1)) * 4;
     return src;
 }
@@ -92,9 +103,10 @@ struct Prefetch {
     float sc;  // threads 0..63: sK of key tid; 64..127: sV of key tid-64
 };
 
-// Thread t loads 16-byte K chunk t + 256 n (row (t + 256 n) / (D/16)) and the
-// 4x4 int8 V block t + 256 n (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3); in
-// both cases consecutive n are 4096 bytes apart.
+// Thread t loads 16-byte K chunk t + 256 n (row (t + 256 n) / (D/16); chunks
+// of consecutive n are 4096 bytes apart) and the 4x4 int8 V block t + 256 n
+// (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3; blocks of consecutive n are
+// 16 dim groups = 64 bytes apart).
 template <int D>
 __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& src, int k0) {
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
@@ -108,7 +120,7 @@ __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& sr
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             pf.v[n][i] = __builtin_amdgcn_raw_buffer_load_b32(src.v, src.voff_v,
-                                                              k0 * D + n * 4096 + i * D, 0);
+                                                              k0 * D + n * 64 + i * D, 0);
     if (threadIdx.x < 2 * kKV)
         pf.sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.s, src.voff_s,
                                                                                k0 * 4, 0));
@@ -127,7 +139,7 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
 #pragma unroll
     for (int n = 0; n < Stage<D>::kVItems; ++n) {
         const int it = t + n * kThreads;
-        const int kg = it / (D / 4), dg = it % (D / 4);
+        const int kg = v_key_group(it), dg = v_dim_group(it);
         const int p0 = vt_pos(4 * kg);
         uint32_t x[4];
 #pragma unroll
