@@ -81,6 +81,20 @@ __device__ __forceinline__ int group8_sum(int v) {
     return v;
 }
 
+// x combined with the value of lane ^ 32: v_permlane32_swap exchanges the two
+// 32-lane halves on the VALU (no LDS round trip as with ds_bpermute); the
+// pair it returns holds x of both lanes in either order.
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Signed byte i (0..3) of a packed dword as fp32 (one SDWA v_cvt_f32_i32).
 template <int I>
 __device__ __forceinline__ float sbyte_to_f32(int w) {

@@ -298,7 +298,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
                             mx = fmaxf(mx, u[T][4 * g + c]);
                         }
                     }
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = max_xor32(mx);
                 if (__ballot(!(mx * qscale <= m + kRescaleSlack))) { slow = true; break; }
                 const float neg_m = -m;
                 const float* sv_l = sk_l + kKV;
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
                         mx = fmaxf(mx, v);
                     }
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = max_xor32(mx);
             const float m_new = fmaxf(m, mx);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
             const float corr = fast_exp2(m - m_use);
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
         ++kt;
     }
 
-    const float L = lsum + __shfl_xor(lsum, 32);
+    const float L = sum_xor32(lsum);
     if (!qok) return;
     const float inv = 1.f / L;
     uint16_t* orow = out + (base + q) * D;
