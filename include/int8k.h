@@ -89,6 +89,36 @@ int int8k_decode_attention_forward_cache(
     int BH, int S, int capacity, int head_dim, int nsplit,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode over a paged INT8 KV cache (no counterpart in the reference, whose
+ * decode is contiguous only — kernels/int8_decode_attention.cu:443-547; this
+ * is the serving layout a page-table caller uses).
+ *
+ *   Q int8 [B, H, D], scale_Q fp32 [B*H]
+ *   K_pages / V_pages int8 [num_pages, H, page_size, D]
+ *   sK_pages / sV_pages fp32 [num_pages, H, page_size]
+ *   block_tables int32 [B, max_pages_per_seq]: page of positions
+ *       [i*page_size, (i+1)*page_size) of sequence b is block_tables[b][i]
+ *   context_lens int32 [B]: sequence b attends to positions 0 .. len-1,
+ *       1 <= len <= max_context (a length of 0 gives a zero output row)
+ *   out fp16 [B, H, D]
+ *
+ * Same math as int8k_decode_attention_forward per (b, h) over the gathered
+ * positions.  page_size must be a power of two in [16, 1024];
+ * max_context <= max_pages_per_seq * page_size.  A page id outside
+ * [0, num_pages) reads page num_pages-1, so a corrupt table reads wrong pages
+ * rather than memory outside the cache.  nsplit as for the contiguous call, planned on
+ * max_context; the workspace comes from
+ * int8k_decode_attention_paged_workspace_bytes. */
+size_t int8k_decode_attention_paged_workspace_bytes(int B, int H, int max_context,
+                                                    int head_dim, int nsplit);
+
+int int8k_decode_attention_forward_paged(
+    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, uint16_t* out,
+    const float* scale_Q, const float* sK_pages, const float* sV_pages,
+    const int32_t* block_tables, const int32_t* context_lens,
+    int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
+    int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* INT8 prefill attention (seq_q == seq_kv).                                 */
 /*                                                                          */

@@ -157,6 +157,55 @@ __device__ __forceinline__ int group_sum(int v) {
     else return group4_sum(v);
 }
 
+// QK^T, online softmax and PV for one wave iteration whose NSLOT rows per
+// group are loaded (kv, vv, sk, sv).  MASKED: rows >= j1 get score -inf and
+// weight 0 (their loads point at some valid row).
+template <int D, int NS, bool MASKED>
+__device__ __forceinline__ void decode_math(const Int4 (&kv)[NS], const Int4 (&vv)[NS],
+                                            const float (&sk)[NS], const float (&sv)[NS],
+                                            int row0, int j1, const Int4& q, float qscale,
+                                            float& m, float& l, float* acc) {
+    // QK^T: exact int32 dot per row, summed over the LPR lanes of the group.
+    float sc[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        int d = __builtin_amdgcn_sdot4(q.x, kv[t].x, 0, false);
+        d = __builtin_amdgcn_sdot4(q.y, kv[t].y, d, false);
+        d = __builtin_amdgcn_sdot4(q.z, kv[t].z, d, false);
+        d = __builtin_amdgcn_sdot4(q.w, kv[t].w, d, false);
+        d = group_sum<D>(d);
+        sc[t] = static_cast<float>(d) * qscale * sk[t];
+        if constexpr (MASKED) {
+            if (row0 + t >= j1) sc[t] = -INFINITY;
+        }
+    }
+
+    // Online softmax (log2 domain) for this group's NSLOT rows.
+    float mx = sc[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) mx = fmaxf(mx, sc[t]);
+    const float m_new = fmaxf(m, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float corr = fast_exp2(m - m_use);
+    l *= corr;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        const float p = fast_exp2(sc[t] - m_use);
+        l += p;
+        float w = p * sv[t];
+        if constexpr (MASKED) {
+            if (row0 + t >= j1) w = 0.f;
+        }
+        fma_bytes(acc + 0, vv[t].x, w);
+        fma_bytes(acc + 4, vv[t].y, w);
+        fma_bytes(acc + 8, vv[t].z, w);
+        fma_bytes(acc + 12, vv[t].w, w);
+    }
+    m = m_new;
+}
+
 // One wave iteration over NSLOT rows per group.  MASKED handles the last
 // partial block of a chunk: rows >= j1 get score -inf and weight 0 (their
 // loads are redirected to row j1-1, which is in bounds).
@@ -209,45 +258,56 @@ __device__ __forceinline__ void decode_iter(
         }
     }
 
-    // QK^T: exact int32 dot per row, summed over the LPR lanes of the group.
-    float sc[NS];
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-        int d = __builtin_amdgcn_sdot4(q.x, kv[t].x, 0, false);
-        d = __builtin_amdgcn_sdot4(q.y, kv[t].y, d, false);
-        d = __builtin_amdgcn_sdot4(q.z, kv[t].z, d, false);
-        d = __builtin_amdgcn_sdot4(q.w, kv[t].w, d, false);
-        d = group_sum<D>(d);
-        sc[t] = static_cast<float>(d) * qscale * sk[t];
-        if constexpr (MASKED) {
-            if (row0 + t >= j1) sc[t] = -INFINITY;
-        }
-    }
+    decode_math<D, NS, MASKED>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
+}
 
-    // Online softmax (log2 domain) for this group's NSLOT rows.
-    float mx = sc[0];
+// Merges the G row-group states of a wave (lanes with equal `sub`) and writes
+// the unit's partial state, or with FINAL the normalised fp16 row (a unit that
+// saw no rows, L == 0, gives zeros).
+template <int D, bool FINAL>
+__device__ __forceinline__ void finish_unit(float m, float l, float* acc, int grp, int sub,
+                                            int unit, float* __restrict__ part_ml,
+                                            float* __restrict__ part_acc,
+                                            uint16_t* __restrict__ out) {
+    constexpr int LPR = D / 16;
+    float M = m;
 #pragma unroll
-    for (int t = 1; t < NS; ++t) mx = fmaxf(mx, sc[t]);
-    const float m_new = fmaxf(m, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float corr = fast_exp2(m - m_use);
-    l *= corr;
+    for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+    const float f = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
+    float L = l * f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] *= corr;
+    for (int e = 0; e < 16; ++e) acc[e] *= f;
 #pragma unroll
-    for (int t = 0; t < NS; ++t) {
-        const float p = fast_exp2(sc[t] - m_use);
-        l += p;
-        float w = p * sv[t];
-        if constexpr (MASKED) {
-            if (row0 + t >= j1) w = 0.f;
-        }
-        fma_bytes(acc + 0, vv[t].x, w);
-        fma_bytes(acc + 4, vv[t].y, w);
-        fma_bytes(acc + 8, vv[t].z, w);
-        fma_bytes(acc + 12, vv[t].w, w);
+    for (int off = LPR; off < 64; off <<= 1) {
+        L += __shfl_xor(L, off);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
     }
-    m = m_new;
+    if constexpr (FINAL) {
+        if (grp == 0) {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            uint16_t h[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) h[e] = f32_to_f16_bits(acc[e] * inv);
+            uint4* dst = reinterpret_cast<uint4*>(out + (size_t)unit * D + sub * 16);
+            dst[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                h[6] | (h[7] << 16));
+            dst[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16),
+                                h[12] | (h[13] << 16), h[14] | (h[15] << 16));
+        }
+        return;
+    }
+    if (grp == 0) {
+        float4* dst = reinterpret_cast<float4*>(part_acc + (size_t)unit * D + sub * 16);
+        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+        dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+        if (sub == 0) {
+            part_ml[2 * (size_t)unit] = M;
+            part_ml[2 * (size_t)unit + 1] = L;
+        }
+    }
 }
 
 // Pass 1: one wave per (bh, split); writes the unnormalised partial state,
@@ -300,45 +360,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
         decode_iter<D, NS, true, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, base + grp * NS, j1, sub,
                                                  q, qscale, m, l, acc);
 
-    // Merge the G row-group states of this wave (lanes with equal `sub`).
-    float M = m;
-#pragma unroll
-    for (int off = G::kLanesPerRow; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
-    const float f = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
-    float L = l * f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] *= f;
-#pragma unroll
-    for (int off = G::kLanesPerRow; off < 64; off <<= 1) {
-        L += __shfl_xor(L, off);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
-    }
-    if constexpr (FINAL) {
-        if (grp == 0) {
-            const float inv = 1.f / L;
-            uint16_t h[16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) h[e] = f32_to_f16_bits(acc[e] * inv);
-            uint4* dst = reinterpret_cast<uint4*>(out + (size_t)unit * D + sub * 16);
-            dst[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                                h[6] | (h[7] << 16));
-            dst[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16),
-                                h[12] | (h[13] << 16), h[14] | (h[15] << 16));
-        }
-        return;
-    }
-    if (grp == 0) {
-        float4* dst = reinterpret_cast<float4*>(part_acc + (size_t)unit * D + sub * 16);
-        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-        dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
-        dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
-        if (sub == 0) {
-            part_ml[2 * (size_t)unit] = M;
-            part_ml[2 * (size_t)unit + 1] = L;
-        }
-    }
+    finish_unit<D, FINAL>(m, l, acc, grp, sub, unit, part_ml, part_acc, out);
 }
 
 // Pass 2: one wave per bh merges its nsplit partial states into fp16.
@@ -372,10 +394,89 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 #pragma unroll
         for (int i = 0; i < DPL; ++i) acc[i] = fmaf(pa[(size_t)s * D + i], w, acc[i]);
     }
-    const float inv = 1.f / L;
+    const float inv = L > 0.f ? 1.f / L : 0.f;  // no rows at all (empty sequence): zeros
 #pragma unroll
     for (int i = 0; i < DPL; ++i)
         out[(size_t)bh * D + lane * DPL + i] = f32_to_f16_bits(acc[i] * inv);
+}
+
+// Paged variant of pass 1.  Unit = (b, h, split) as above, over positions
+// [j0, j1) of sequence b (j1 <= context_lens[b]).  A group's NSLOT rows are
+// NSLOT-aligned and page_size is a multiple of NSLOT, so they sit in one
+// page: one table lookup per group per iteration, then the same immediate
+// slot offsets as the contiguous kernel.  Page p of head h holds
+// K/V [p][h][page_size][D] and scales [p][h][page_size].
+template <int D, int NS, bool FINAL>
+__global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ Kp,
+    const int8_t* __restrict__ Vp, const float* __restrict__ sQ,
+    const float* __restrict__ sKp, const float* __restrict__ sVp,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    float* __restrict__ part_ml, float* __restrict__ part_acc, uint16_t* __restrict__ out,
+    int H, int num_pages, int log2_page, int max_pages, int nsplit, int chunk, int units,
+    float qk_scale_log2) {
+    using G = DecodeGeom<D, NS>;
+    const int lane = threadIdx.x & 63;
+    const int unit = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (unit >= units) return;  // whole wave exits; no block barrier below
+    const int bh = unit / nsplit;
+    const int sp = unit - bh * nsplit;
+    const int b = bh / H, hh = bh - b * H;
+    const int page = 1 << log2_page;
+    const int len = min(context_lens[b], max_pages << log2_page);
+    const int j0 = sp * chunk;
+    const int j1 = min(len, j0 + chunk);
+
+    const int sub = lane % G::kLanesPerRow;
+    const int grp = lane / G::kLanesPerRow;
+    const Int4 q = load16(Q + (size_t)bh * D + sub * 16);
+    const float qscale = sQ[bh] * qk_scale_log2;
+    const int32_t* table = block_tables + (size_t)b * max_pages;
+    // element offset of row r of this head (an id outside [0, num_pages) reads the last page)
+    auto row_off = [&](int r) -> size_t {
+        const int pg = min((unsigned)table[r >> log2_page], (unsigned)(num_pages - 1));
+        return ((size_t)pg * H + hh) * page + (r & (page - 1));
+    };
+
+    float m = -INFINITY, l = 0.f;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
+    for (int k = 0; k < n_full; ++k) {
+        const int row0 = j0 + k * G::kRowsPerIter + grp * NS;
+        const size_t r0 = row_off(row0);
+        const int8_t* kp = Kp + r0 * D + sub * 16;
+        const int8_t* vp = Vp + r0 * D + sub * 16;
+        Int4 kv[NS], vv[NS];
+        float sk[NS], sv[NS];
+#pragma unroll
+        for (int t = 0; t < NS; ++t) kv[t] = load_kv16<true>(kp + t * D);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) vv[t] = load_kv16<true>(vp + t * D);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            sk[t] = sKp[r0 + t];
+            sv[t] = sVp[r0 + t];
+        }
+        decode_math<D, NS, false>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
+    }
+    const int base = j0 + n_full * G::kRowsPerIter;
+    if (base < j1) {
+        const int row0 = base + grp * NS;
+        Int4 kv[NS], vv[NS];
+        float sk[NS], sv[NS];
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const size_t r = row_off(min(row0 + t, j1 - 1));
+            kv[t] = load_kv16<true>(Kp + r * D + sub * 16);
+            vv[t] = load_kv16<true>(Vp + r * D + sub * 16);
+            sk[t] = sKp[r];
+            sv[t] = sVp[r];
+        }
+        decode_math<D, NS, true>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
+    }
+    finish_unit<D, FINAL>(m, l, acc, grp, sub, unit, part_ml, part_acc, out);
 }
 
 struct DecodeWorkspace {
@@ -454,6 +555,34 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     return check_launch("decode_combine_kernel");
 }
 
+template <int D>
+int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, uint16_t* out,
+                        const float* sQ, const float* sKp, const float* sVp,
+                        const int32_t* tables, const int32_t* lens, int B, int H,
+                        int num_pages, int log2_page, int max_pages, const SplitPlan& plan,
+                        const DecodeWorkspace& w, hipStream_t stream) {
+    const int BH = B * H;
+    const long long units = (long long)BH * plan.nsplit;
+    const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
+    const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
+    constexpr int NS = D == 128 ? 8 : 4;
+    const bool final_pass = plan.nsplit == 1 && aligned_to(out, 16);
+    if (final_pass)
+        decode_paged_kernel<D, NS, true><<<grid, kBlockThreads, 0, stream>>>(
+            Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,
+            log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk);
+    else
+        decode_paged_kernel<D, NS, false><<<grid, kBlockThreads, 0, stream>>>(
+            Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,
+            log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk);
+    int st = check_launch("decode_paged_kernel");
+    if (st != INT8K_OK || final_pass) return st;
+    const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));
+    decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out, BH,
+                                                                  plan.nsplit);
+    return check_launch("decode_combine_kernel");
+}
+
 }  // namespace
 }  // namespace int8k
 
@@ -511,4 +640,75 @@ extern "C" int int8k_decode_attention_forward_cache(
     void* workspace, size_t workspace_bytes, void* stream) {
     return decode_impl(Q, K_cache, V_cache, out, scale_Q, sK_cache, sV_cache, BH, S, capacity,
                        head_dim, nsplit, workspace, workspace_bytes, stream);
+}
+
+// The paged kernel always uses 8 slots for D = 128 and 4 for D = 64 (page_size
+// is a multiple of both), so its split plan is computed for those slot counts.
+static SplitPlan plan_paged(int BH, int max_context, int D, int nsplit_req) {
+    const int ns_slots = D == 128 ? 8 : 4;
+    const int R = rows_per_iter(D, ns_slots);
+    const DecodeTuning tn = tuning_for(D);
+    const long long max_split = ceil_div(max_context, R);
+    long long ns;
+    if (nsplit_req > 0) {
+        ns = nsplit_req;
+    } else {
+        ns = ceil_div(tn.target_units, BH);
+        ns = std::min(ns, std::max<long long>(1, ceil_div(max_context, 4LL * R)));
+    }
+    ns = std::max<long long>(1, std::min(ns, max_split));
+    const long long chunk = round_up((size_t)ceil_div(max_context, ns), (size_t)R);
+    ns = ceil_div(max_context, chunk);
+    return SplitPlan{(int)ns, (int)chunk};
+}
+
+extern "C" size_t int8k_decode_attention_paged_workspace_bytes(int B, int H, int max_context,
+                                                               int head_dim, int nsplit) {
+    if (B <= 0 || H <= 0 || max_context <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
+    const long long BH = (long long)B * H;
+    if (BH >= (1LL << 31)) return 0;
+    const SplitPlan plan = plan_paged((int)BH, max_context, head_dim, nsplit);
+    return carve(nullptr, BH * plan.nsplit, head_dim).bytes;
+}
+
+extern "C" int int8k_decode_attention_forward_paged(
+    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, uint16_t* out,
+    const float* scale_Q, const float* sK_pages, const float* sV_pages,
+    const int32_t* block_tables, const int32_t* context_lens,
+    int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
+    int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_last_error();
+    if (!Q || !K_pages || !V_pages || !out || !scale_Q || !sK_pages || !sV_pages ||
+        !block_tables || !context_lens)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (B <= 0 || H <= 0 || num_pages <= 0 || max_pages_per_seq <= 0 || max_context <= 0 ||
+        nsplit < 0)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (head_dim != 64 && head_dim != 128) return INT8K_ERR_UNSUPPORTED;
+    if (page_size < 16 || page_size > 1024 || (page_size & (page_size - 1)) != 0)
+        return INT8K_ERR_UNSUPPORTED;
+    if ((long long)max_context > (long long)max_pages_per_seq * page_size)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    const long long BH = (long long)B * H;
+    if ((long long)num_pages * H * page_size * head_dim >= (1LL << 40)) return INT8K_ERR_UNSUPPORTED;
+    if (!aligned_to(Q, 16) || !aligned_to(K_pages, 16) || !aligned_to(V_pages, 16) ||
+        !aligned_to(scale_Q, 4) || !aligned_to(sK_pages, 4) || !aligned_to(sV_pages, 4) ||
+        !aligned_to(block_tables, 4) || !aligned_to(context_lens, 4) || !aligned_to(out, 2))
+        return INT8K_ERR_MISALIGNED;
+    if (BH >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    const SplitPlan plan = plan_paged((int)BH, max_context, head_dim, nsplit);
+    const long long units = BH * plan.nsplit;
+    if (units >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    const DecodeWorkspace w = carve(workspace, units, head_dim);
+    if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
+    if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;
+    int log2_page = 0;
+    while ((1 << log2_page) < page_size) ++log2_page;
+    if (head_dim == 128)
+        return launch_decode_paged<128>(Q, K_pages, V_pages, out, scale_Q, sK_pages, sV_pages,
+                                        block_tables, context_lens, B, H, num_pages, log2_page,
+                                        max_pages_per_seq, plan, w, as_stream(stream));
+    return launch_decode_paged<64>(Q, K_pages, V_pages, out, scale_Q, sK_pages, sV_pages,
+                                   block_tables, context_lens, B, H, num_pages, log2_page,
+                                   max_pages_per_seq, plan, w, as_stream(stream));
 }

@@ -488,6 +488,58 @@ torch::Tensor int8_decode_attention_forward_cache_torch(torch::Tensor Q, torch::
     return out;
 }
 
+// Decode over a paged int8 KV cache (no reference counterpart): K/V pages
+// [num_pages, H, page, D], scale pages [num_pages, H, page], block_tables
+// [B, max_pages] int32, context_lens [B] int32 (each in [1, max_context]).
+torch::Tensor int8_decode_attention_forward_paged_torch(
+    torch::Tensor Q, torch::Tensor K_pages, torch::Tensor V_pages, torch::Tensor scale_Q,
+    torch::Tensor sK_pages, torch::Tensor sV_pages, torch::Tensor block_tables,
+    torch::Tensor context_lens, int64_t max_context) {
+    TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
+    TORCH_CHECK(Q.dtype() == torch::kInt8 && K_pages.dtype() == torch::kInt8 &&
+                    V_pages.dtype() == torch::kInt8,
+                "Q/K/V must be int8");
+    TORCH_CHECK(Q.is_contiguous() && K_pages.is_contiguous() && V_pages.is_contiguous(),
+                "Q/K/V must be contiguous");
+    TORCH_CHECK(Q.dim() == 3 && K_pages.dim() == 4 && K_pages.sizes() == V_pages.sizes(),
+                "expected Q (batch, heads, head_dim), pages (num_pages, heads, page, head_dim)");
+    const int64_t B = Q.size(0), H = Q.size(1), D = Q.size(2);
+    const int64_t NP = K_pages.size(0), P = K_pages.size(2);
+    TORCH_CHECK(K_pages.size(1) == H && K_pages.size(3) == D, "Q/K head/dim mismatch");
+    TORCH_CHECK(D == 64 || D == 128, "decode kernel supports head_dim 64 or 128");
+    TORCH_CHECK(block_tables.dtype() == torch::kInt32 && context_lens.dtype() == torch::kInt32,
+                "block_tables and context_lens must be int32");
+    TORCH_CHECK(block_tables.dim() == 2 && block_tables.size(0) == B && context_lens.numel() == B,
+                "block_tables (batch, max_pages) / context_lens (batch,) shape mismatch");
+    TORCH_CHECK(scale_Q.dtype() == torch::kFloat32 && sK_pages.dtype() == torch::kFloat32 &&
+                    sV_pages.dtype() == torch::kFloat32,
+                "scales must be float32");
+    TORCH_CHECK(scale_Q.numel() == B * H && sK_pages.numel() == NP * H * P &&
+                    sV_pages.numel() == NP * H * P,
+                "scale sizes mismatch");
+    const int64_t max_pages = block_tables.size(1);
+    TORCH_CHECK(max_context >= 1 && max_context <= max_pages * P,
+                "max_context must be in [1, max_pages * page_size]");
+    auto sQ = scale_Q.contiguous();
+    auto sK = sK_pages.contiguous();
+    auto sV = sV_pages.contiguous();
+    auto bt = block_tables.contiguous();
+    auto cl = context_lens.contiguous();
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
+    auto out = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
+    const size_t ws_bytes = int8k_decode_attention_paged_workspace_bytes(
+        (int)B, (int)H, (int)max_context, (int)D, 0);
+    auto ws = workspace(ws_bytes, Q.device());
+    const int st = int8k_decode_attention_forward_paged(
+        Q.data_ptr<int8_t>(), K_pages.data_ptr<int8_t>(), V_pages.data_ptr<int8_t>(),
+        reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
+        sK.data_ptr<float>(), sV.data_ptr<float>(), bt.data_ptr<int32_t>(),
+        cl.data_ptr<int32_t>(), (int)B, (int)H, (int)D, (int)NP, (int)P, (int)max_pages,
+        (int)max_context, 0, ws.data_ptr(), ws_bytes, current_stream(Q));
+    check_status(st, "int8_decode_attention_forward_paged");
+    return out;
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("int8_attention_forward", &int8_attention_forward_torch,
           "INT8 attention with per-token quantization — returns FP16 (optional is_causal)",
@@ -521,6 +573,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Per-token (last dim) int8 quantization — returns (int8, fp32 scales)");
     m.def("kv_cache_append", &kv_cache_append_torch,
           "Quantize new K/V tokens into an int8 KV cache at position pos (in place)");
+    m.def("int8_decode_attention_forward_paged", &int8_decode_attention_forward_paged_torch,
+          "INT8 decode attention over a paged KV cache (block tables, per-sequence lengths)");
     m.def("int8_decode_attention_forward_cache", &int8_decode_attention_forward_cache_torch,
           "INT8 decode attention over the first seq_len positions of a KV cache — returns FP16");
     m.attr("abi_version") = int8k_abi_version();

@@ -50,6 +50,9 @@ _SIGNATURES = {
     "int8k_dequantize_int8_to_fp16": (_I, [_P, _P, _F, _LL, _P]),
     "int8k_quantize_per_token": (_I, [_P, _I, _P, _P, _LL, _I, _P]),
     "int8k_kv_cache_append": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "int8k_decode_attention_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "int8k_decode_attention_forward_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                                  _I, _I, _I, _I, _I, _P, _SZ, _P]),
 }
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
@@ -290,4 +293,29 @@ def decode_attention_cache(Qi, K_cache, V_cache, sQ, sK_cache, sV_cache, S, nspl
         _ptr(Qi), _ptr(K_cache), _ptr(V_cache), _ptr(out), _ptr(sQ), _ptr(sK_cache),
         _ptr(sV_cache), BH, S, cap, D, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
     check("int8k_decode_attention_forward_cache", st)
+    return out
+
+
+def decode_paged_workspace_bytes(B, H, max_context, D, nsplit=0):
+    return load().int8k_decode_attention_paged_workspace_bytes(B, H, max_context, D, nsplit)
+
+
+def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_tables,
+                           context_lens, max_context, nsplit=0, out=None):
+    """Decode over a paged cache: K/V_pages [num_pages, H, page, D] int8, scales
+    [num_pages, H, page] fp32, block_tables [B, max_pages] int32, context_lens [B] int32.
+    Returns fp16 [B, H, D]."""
+    import torch
+
+    num_pages, H, page, D = K_pages.shape
+    B, max_pages = block_tables.shape
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.float16, device=Qi.device)
+    ws = torch.empty(max(decode_paged_workspace_bytes(B, H, max_context, D, nsplit), 1),
+                     dtype=torch.uint8, device=Qi.device)
+    st = load().int8k_decode_attention_forward_paged(
+        _ptr(Qi), _ptr(K_pages), _ptr(V_pages), _ptr(out), _ptr(sQ), _ptr(sK_pages),
+        _ptr(sV_pages), _ptr(block_tables), _ptr(context_lens), B, H, D, num_pages, page,
+        max_pages, max_context, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
+    check("int8k_decode_attention_forward_paged", st)
     return out

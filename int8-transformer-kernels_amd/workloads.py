@@ -96,3 +96,38 @@ def mlp_case(T: int, d_model: int, d_ff: int, seed: int, device="cuda", gen_devi
     W2i, sW2 = quantize_per_channel_w(_normal((d_ff, d_model), g, gen_device) * w_std)
     return dict(x=xi.reshape(1, T, d_model).to(device), sx=sx.to(device), W1=W1i.to(device),
                 sW1=sW1.to(device), W2=W2i.to(device), sW2=sW2.to(device))
+
+
+def paged_case(B: int, H: int, D: int, page: int, lens, seed: int, spare_pages: int = 3,
+               device="cuda", gen_device=None):
+    """A paged INT8 KV cache holding B sequences of lengths `lens` (per-token quantized
+    N(0,1) K/V), its pages in a seeded random physical order, plus spare pages filled with
+    other data.  Returns Qi [B,H,D], sQ [B,H], K/V_pages [NP,H,page,D], sK/sV_pages
+    [NP,H,page], block_tables [B, max_pages] int32 (unused entries point at spare pages),
+    context_lens [B] int32."""
+    gen_device = gen_device or device
+    g = torch.Generator(device=gen_device).manual_seed(seed)
+    lens = [int(n) for n in lens]
+    max_pages = max(1, max((n + page - 1) // page for n in lens))
+    n_used = sum((n + page - 1) // page for n in lens)
+    NP = n_used + spare_pages
+    Qi, sQ = quantize_per_token(_normal((B, H, D), g, gen_device).half())
+    pages = {}
+    for name in ("K", "V"):
+        q, s = quantize_per_token(_normal((NP, H, page, D), g, gen_device))
+        pages[name] = (q.to(device), s.to(device))
+    perm = torch.randperm(NP, generator=torch.Generator().manual_seed(seed)).tolist()
+    tables = torch.empty((B, max_pages), dtype=torch.int32)
+    nxt = 0
+    for b, n in enumerate(lens):
+        need = (n + page - 1) // page
+        for i in range(max_pages):
+            if i < need:
+                tables[b, i] = perm[nxt]
+                nxt += 1
+            else:
+                tables[b, i] = perm[n_used + (i % max(spare_pages, 1))] if spare_pages else perm[0]
+    return dict(Qi=Qi.to(device), sQ=sQ.to(device), K_pages=pages["K"][0], sK_pages=pages["K"][1],
+                V_pages=pages["V"][0], sV_pages=pages["V"][1], block_tables=tables.to(device),
+                context_lens=torch.tensor(lens, dtype=torch.int32, device=device),
+                max_context=max(lens), page=page)

@@ -26,6 +26,10 @@ How each function is pinned (tests/test_oracle.py):
   mlp_forward : stage-by-stage against the pieces above on small shapes plus
       KATs (zero input -> zero output codes; constant input -> one code).
   quantize_fp16_per_tensor / dequantize_int8_to_fp16 : closed form + KATs.
+  gather_paged_kv / decode_attention_paged : identity block tables over a
+      contiguous cache reproduce decode_attention exactly; a permuted table
+      with permuted pages gives the same result; positions past a sequence's
+      length never enter (changing them changes nothing).
 No function is left "parity unpinned".
 """
 from __future__ import annotations
@@ -109,6 +113,39 @@ def decode_attention(Qi, Ki, Vi, sQ, sK, sV):
     p = np.exp(scores)
     p /= p.sum(axis=1, keepdims=True)
     return np.einsum("bs,bsd->bd", p, v)
+
+
+def gather_paged_kv(pages, block_tables, context_len, b, page_size):
+    """Positions 0 .. context_len-1 of sequence b from a paged array
+    [num_pages, H, page_size, ...]: position j is pages[block_tables[b][j // page_size], :,
+    j % page_size].  Returns [H, context_len, ...].  No reference counterpart (its decode is
+    contiguous only, kernels/int8_decode_attention.cu:443-547); this is the layout contract of
+    int8k_decode_attention_forward_paged."""
+    pages = np.asarray(pages)
+    j = np.arange(context_len)
+    pg = np.asarray(block_tables)[b][j // page_size]
+    return np.moveaxis(pages[pg, :, j % page_size], 0, 1)
+
+
+def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_tables,
+                           context_lens):
+    """decode_attention per sequence over its gathered pages.
+    Qi [B, H, D]; K/V_pages [num_pages, H, P, D]; sQ [B, H]; sK/sV_pages [num_pages, H, P];
+    block_tables [B, max_pages]; context_lens [B].  Returns float64 [B, H, D]."""
+    Qi = np.asarray(Qi)
+    B, H, D = Qi.shape
+    P = np.asarray(K_pages).shape[2]
+    out = np.zeros((B, H, D))
+    for b in range(B):
+        n = int(context_lens[b])
+        if n <= 0:
+            continue
+        k = gather_paged_kv(K_pages, block_tables, n, b, P)
+        v = gather_paged_kv(V_pages, block_tables, n, b, P)
+        sk = gather_paged_kv(sK_pages, block_tables, n, b, P)
+        sv = gather_paged_kv(sV_pages, block_tables, n, b, P)
+        out[b] = decode_attention(Qi[b], k, v, np.asarray(sQ)[b], sk, sv)
+    return out
 
 
 def prefill_attention(Qi, Ki, Vi, sQ, sK, sV, causal=False):

@@ -288,3 +288,51 @@ def test_quant_utils_per_tensor():
     np.testing.assert_array_equal(q0, 0)  # the 1e-8 guard (reference returns -128 here)
     d = O.dequantize_int8_to_fp16(np.array([-128, 0, 127], np.int8), np.float32(0.5))
     np.testing.assert_array_equal(d, np.array([-64.0, 0.0, 63.5], np.float16))
+
+
+def _contiguous_as_pages(K, P):
+    """[B, H, S, D] -> pages [B*npp, H, P, D] with sequence b in pages b*npp .. (b+1)*npp-1."""
+    B, H, S = K.shape[:3]
+    npp = -(-S // P)
+    pad = np.zeros((B, H, npp * P) + K.shape[3:], K.dtype)
+    pad[:, :, :S] = K
+    pages = pad.reshape((B, H, npp, P) + K.shape[3:])
+    pages = np.moveaxis(pages, 2, 1).reshape((B * npp, H, P) + K.shape[3:])
+    tables = np.arange(B * npp, dtype=np.int32).reshape(B, npp)
+    return pages, tables
+
+
+def test_paged_decode_identity_tables_equal_contiguous():
+    rng = np.random.default_rng(5)
+    B, H, S, D, P = 2, 3, 50, 16, 16
+    Q = rng.integers(-127, 128, (B, H, D), dtype=np.int8)
+    K = rng.integers(-127, 128, (B, H, S, D), dtype=np.int8)
+    V = rng.integers(-127, 128, (B, H, S, D), dtype=np.int8)
+    sQ = rng.uniform(0.001, 0.02, (B, H)).astype(np.float32)
+    sK = rng.uniform(0.001, 0.02, (B, H, S)).astype(np.float32)
+    sV = rng.uniform(0.001, 0.02, (B, H, S)).astype(np.float32)
+    Kp, tables = _contiguous_as_pages(K, P)
+    Vp, _ = _contiguous_as_pages(V, P)
+    sKp, _ = _contiguous_as_pages(sK, P)
+    sVp, _ = _contiguous_as_pages(sV, P)
+    lens = np.array([S, S], np.int32)
+    got = O.decode_attention_paged(Q, Kp, Vp, sQ, sKp, sVp, tables, lens)
+    ref = O.decode_attention(Q.reshape(B * H, D), K.reshape(B * H, S, D), V.reshape(B * H, S, D),
+                             sQ.reshape(-1), sK.reshape(B * H, S), sV.reshape(B * H, S))
+    np.testing.assert_allclose(got.reshape(B * H, D), ref, rtol=0, atol=1e-12)
+    # a permuted physical order with the table permuted alike changes nothing
+    perm = rng.permutation(Kp.shape[0])
+    inv = np.argsort(perm)
+    got2 = O.decode_attention_paged(Q, Kp[perm], Vp[perm], sQ, sKp[perm], sVp[perm],
+                                    inv[tables].astype(np.int32), lens)
+    np.testing.assert_array_equal(got2, got)
+    # positions past a sequence's length never enter
+    lens3 = np.array([17, 33], np.int32)
+    a = O.decode_attention_paged(Q, Kp, Vp, sQ, sKp, sVp, tables, lens3)
+    Kp2 = Kp.copy()
+    Kp2[1, :, 1:] = 99          # sequence 0, positions 17.. (page 1, rows 1..)
+    Kp2[tables[1][2], :, 1:] = -99  # sequence 1, positions 33..
+    b_ = O.decode_attention_paged(Q, Kp2, Vp, sQ, sKp, sVp, tables, lens3)
+    np.testing.assert_array_equal(a, b_)
+    ref3 = O.decode_attention(Q[1], K[1, :, :33], V[1, :, :33], sQ[1], sK[1, :, :33], sV[1, :, :33])
+    np.testing.assert_allclose(a[1], ref3, rtol=0, atol=1e-12)

@@ -1,0 +1,115 @@
+"""Decode over a paged INT8 KV cache (GPU tests).
+
+Checked against the CPU oracle's gather-then-decode restatement at the attention
+tolerances, against the contiguous decode kernel on the same data, and for the
+documented edge behaviour: ragged lengths (1, page-1, page+1, non-multiples of the
+64-row wave iteration), forced split counts, a zero-length sequence and out-of-range
+page ids (any id outside [0, num_pages) reads the last page instead of memory outside
+the cache).
+"""
+import numpy as np
+import pytest
+import torch
+
+import int8k_capi as capi
+import workloads
+from helpers import assert_attn_close
+from oracle import int8_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(c):
+    return O.decode_attention_paged(*(c[k].cpu().numpy() for k in (
+        "Qi", "K_pages", "V_pages", "sQ", "sK_pages", "sV_pages", "block_tables",
+        "context_lens")))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("page", [16, 64, 256])
+def test_paged_decode_matches_oracle(gpu, D, page):
+    lens = [1, page - 1, page + 1, 200, 777, 1024]
+    c = workloads.paged_case(len(lens), 4, D, page, lens, seed=page + D, device=gpu)
+    out = capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                      c["sK_pages"], c["sV_pages"], c["block_tables"],
+                                      c["context_lens"], c["max_context"])
+    torch.cuda.synchronize()
+    assert_attn_close(out.float().cpu().numpy(), _oracle(c))
+
+
+def test_paged_decode_via_torch_op(ext, gpu):
+    lens = [300, 5, 4096]
+    c = workloads.paged_case(3, 8, 128, 16, lens, seed=9, device=gpu)
+    out = ext.int8_decode_attention_forward_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                                  c["sK_pages"], c["sV_pages"],
+                                                  c["block_tables"], c["context_lens"],
+                                                  c["max_context"])
+    torch.cuda.synchronize()
+    assert out.shape == (3, 8, 128) and out.dtype == torch.float16
+    assert_attn_close(out.float().cpu().numpy(), _oracle(c))
+
+
+@pytest.mark.parametrize("nsplit", [1, 2, 7, 64])
+def test_paged_decode_forced_splits(gpu, nsplit):
+    lens = [1000, 64, 513]
+    c = workloads.paged_case(3, 2, 128, 32, lens, seed=nsplit, device=gpu)
+    out = capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                      c["sK_pages"], c["sV_pages"], c["block_tables"],
+                                      c["context_lens"], c["max_context"], nsplit=nsplit)
+    torch.cuda.synchronize()
+    assert_attn_close(out.float().cpu().numpy(), _oracle(c))
+
+
+def test_paged_equals_contiguous_kernel(gpu):
+    # identity page tables over a contiguous cache: same positions, same math
+    B, H, D, S, P = 2, 4, 128, 640, 64
+    case = workloads.decode_case(B, H, D, S, seed=3, device=gpu)
+    npp = S // P
+
+    def pages(x):  # [B, H, S, ...] -> [B*npp, H, P, ...]
+        x = x.reshape((B, H, npp, P) + tuple(x.shape[3:]))
+        return x.movedim(2, 1).reshape((B * npp, H, P) + tuple(x.shape[4:])).contiguous()
+
+    tables = torch.arange(B * npp, dtype=torch.int32, device=gpu).reshape(B, npp)
+    lens = torch.full((B,), S, dtype=torch.int32, device=gpu)
+    out = capi.decode_attention_paged(case["Qi"], pages(case["Ki"]), pages(case["Vi"]),
+                                      case["sQ"], pages(case["sK"]), pages(case["sV"]), tables,
+                                      lens, S)
+    ref = capi.decode_attention(case["Qi"].reshape(B * H, D), case["Ki"].reshape(B * H, S, D),
+                                case["Vi"].reshape(B * H, S, D), case["sQ"].reshape(-1),
+                                case["sK"].reshape(-1), case["sV"].reshape(-1))
+    torch.cuda.synchronize()
+    d = (out.reshape(B * H, D).float() - ref.float()).abs().max().item()
+    assert d <= 2e-3, d
+
+
+def test_paged_decode_zero_length_and_clamped_pages(gpu):
+    lens = [0, 100, 40]
+    c = workloads.paged_case(3, 2, 64, 16, lens, seed=4, device=gpu)
+    NP = c["K_pages"].shape[0]
+    bt = c["block_tables"].clone()
+    bt[2, 1] = NP + 5          # positions 16..31 of sequence 2 -> clamped to page NP-1
+    bt[2, 2] = -3              # positions 32..39 -> also page NP-1 (any id outside [0, NP))
+    out = capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                      c["sK_pages"], c["sV_pages"], bt, c["context_lens"],
+                                      c["max_context"])
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert np.all(o[0] == 0)
+    bt_ref = torch.where((bt < 0) | (bt >= NP), torch.full_like(bt, NP - 1), bt)
+    ref = _oracle(dict(c, block_tables=bt_ref))
+    assert_attn_close(o[1:], ref[1:])
+
+
+def test_paged_argument_validation(gpu):
+    c = workloads.paged_case(1, 1, 64, 16, [20], seed=1, device=gpu)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        capi.decode_attention_paged(c["Qi"], c["K_pages"][:, :, :12].contiguous(),
+                                    c["V_pages"][:, :, :12].contiguous(), c["sQ"],
+                                    c["sK_pages"][:, :, :12].contiguous(),
+                                    c["sV_pages"][:, :, :12].contiguous(), c["block_tables"],
+                                    c["context_lens"], 20)
+    with pytest.raises(RuntimeError, match="invalid"):
+        capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                    c["sK_pages"], c["sV_pages"], c["block_tables"],
+                                    c["context_lens"], 10 ** 6)
