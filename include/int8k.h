@@ -232,6 +232,33 @@ int int8k_kv_cache_append(const void* k_new, const void* v_new, int dtype,
                           int8_t* K_cache, int8_t* V_cache, float* sK_cache, float* sV_cache,
                           int BH, int n_new, int pos, int capacity, int head_dim, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Producer-fused quantizers (quantize on emit).  The reference quantizes    */
+/* every INT8 kernel input in a separate eager pass after its fp16 producer  */
+/* (bench/bench_block.py:59-63, 104-110, 119-121, 138-139); these do the     */
+/* producer and the quantization in one pass.  No reference counterpart.    */
+/* ------------------------------------------------------------------------ */
+
+/* LayerNorm over the last dim, then per-token int8 (the MLP input):
+ *   y = (x - mean) / sqrt(var + eps) [* gamma] [+ beta]  (fp32, biased var),
+ *   rounded to x's dtype (as F.layer_norm returns it), then
+ *   scales[r] = max(amax_r(y), 1e-8) / 127, q = rn(clamp(y / s, -128, 127)).
+ * x [rows, cols] of `dtype` (int8k_dtype); gamma/beta fp32 [cols] or NULL;
+ * q int8 [rows, cols]; scales fp32 [rows]; y_out [rows, cols] of `dtype`
+ * receives y when non-NULL. */
+int int8k_layernorm_quantize_per_token(const void* x, int dtype, const float* gamma,
+                                       const float* beta, float eps, int8_t* q, float* scales,
+                                       void* y_out, long long rows, int cols, void* stream);
+
+/* Splits a projection output x [B, S, parts, H, head_dim] (parts = 3 for a
+ * fused QKV projection) into heads and quantizes each head row per token:
+ * part p goes to q_p int8 [B, H, S, head_dim] and s_p fp32 [B, H, S] — the
+ * inputs of int8k_attention_forward / the decode calls.  Pointers of parts
+ * >= `parts` are ignored. */
+int int8k_quantize_heads(const void* x, int dtype, int parts, int8_t* q0, float* s0,
+                         int8_t* q1, float* s1, int8_t* q2, float* s2, int B, int S, int H,
+                         int head_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -408,6 +408,66 @@ std::tuple<torch::Tensor, torch::Tensor> quantize_per_token_torch(torch::Tensor 
     return {q, s};
 }
 
+// LayerNorm over the last dim, rounded to x's dtype, then per-token int8:
+// returns (q, scales).  weight/bias optional (any float dtype; used as fp32).
+std::tuple<torch::Tensor, torch::Tensor> layernorm_quantize_per_token_torch(
+    torch::Tensor x, c10::optional<torch::Tensor> weight, c10::optional<torch::Tensor> bias,
+    double eps) {
+    TORCH_CHECK(x.device().is_cuda(), "x must be a CUDA tensor");
+    TORCH_CHECK(x.dim() >= 1 && x.numel() > 0, "x must be a non-empty tensor");
+    const int code = dtype_code(x);
+    auto xc = x.contiguous();
+    const int64_t cols = x.size(-1);
+    TORCH_CHECK(cols <= INT32_MAX, "rows too long");
+    torch::Tensor g, b;
+    if (weight.has_value() && weight->defined()) {
+        TORCH_CHECK(weight->numel() == cols, "weight must have size(-1) elements");
+        g = weight->to(x.device(), torch::kFloat32).contiguous();
+    }
+    if (bias.has_value() && bias->defined()) {
+        TORCH_CHECK(bias->numel() == cols, "bias must have size(-1) elements");
+        b = bias->to(x.device(), torch::kFloat32).contiguous();
+    }
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+    auto q = torch::empty(x.sizes(), torch::TensorOptions().dtype(torch::kInt8).device(x.device()));
+    auto s = torch::empty(x.sizes().slice(0, x.dim() - 1),
+                          torch::TensorOptions().dtype(torch::kFloat32).device(x.device()));
+    check_status(int8k_layernorm_quantize_per_token(
+                     xc.data_ptr(), code, g.defined() ? g.data_ptr<float>() : nullptr,
+                     b.defined() ? b.data_ptr<float>() : nullptr, (float)eps,
+                     q.data_ptr<int8_t>(), s.data_ptr<float>(), nullptr, xc.numel() / cols,
+                     (int)cols, current_stream(x)),
+                 "layernorm_quantize_per_token");
+    return {q, s};
+}
+
+// x (batch, seq, parts * heads * head_dim) -> [q_0, s_0, q_1, s_1, ...] with
+// q_p int8 (batch, heads, seq, head_dim) and s_p fp32 (batch, heads, seq).
+std::vector<torch::Tensor> quantize_heads_torch(torch::Tensor x, int64_t heads, int64_t parts) {
+    TORCH_CHECK(x.device().is_cuda(), "x must be a CUDA tensor");
+    TORCH_CHECK(x.dim() == 3, "x must be (batch, seq, parts * heads * head_dim)");
+    TORCH_CHECK(parts >= 1 && parts <= 3 && heads >= 1, "parts must be 1..3, heads >= 1");
+    TORCH_CHECK(x.size(2) % (parts * heads) == 0, "last dim must be parts * heads * head_dim");
+    const int code = dtype_code(x);
+    auto xc = x.contiguous();
+    const int64_t B = x.size(0), S = x.size(1), Dh = x.size(2) / (parts * heads);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+    std::vector<torch::Tensor> outs;
+    for (int64_t p = 0; p < parts; ++p) {
+        outs.push_back(torch::empty({B, heads, S, Dh},
+                                    torch::TensorOptions().dtype(torch::kInt8).device(x.device())));
+        outs.push_back(torch::empty({B, heads, S},
+                                    torch::TensorOptions().dtype(torch::kFloat32).device(x.device())));
+    }
+    auto qp = [&](int64_t p) { return p < parts ? outs[2 * p].data_ptr<int8_t>() : nullptr; };
+    auto sp = [&](int64_t p) { return p < parts ? outs[2 * p + 1].data_ptr<float>() : nullptr; };
+    check_status(int8k_quantize_heads(xc.data_ptr(), code, (int)parts, qp(0), sp(0), qp(1), sp(1),
+                                      qp(2), sp(2), (int)B, (int)S, (int)heads, (int)Dh,
+                                      current_stream(x)),
+                 "quantize_heads");
+    return outs;
+}
+
 // Quantize k_new/v_new (batch, heads, n_new, head_dim) per token into positions
 // pos .. pos+n_new-1 of the int8 caches (batch, heads, capacity, head_dim) and
 // their fp32 scales (batch, heads, capacity).  In place.
@@ -571,6 +631,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "int8 -> fp16 with a scalar scale");
     m.def("quantize_per_token", &quantize_per_token_torch,
           "Per-token (last dim) int8 quantization — returns (int8, fp32 scales)");
+    m.def("layernorm_quantize_per_token", &layernorm_quantize_per_token_torch,
+          "LayerNorm (last dim) then per-token int8 — returns (int8, fp32 scales)",
+          py::arg("x"), py::arg("weight") = py::none(), py::arg("bias") = py::none(),
+          py::arg("eps") = 1e-5);
+    m.def("quantize_heads", &quantize_heads_torch,
+          "Split (batch, seq, parts*heads*head_dim) into heads and quantize per token — "
+          "returns [q_0, s_0, q_1, s_1, ...]",
+          py::arg("x"), py::arg("heads"), py::arg("parts") = 3);
     m.def("kv_cache_append", &kv_cache_append_torch,
           "Quantize new K/V tokens into an int8 KV cache at position pos (in place)");
     m.def("int8_decode_attention_forward_paged", &int8_decode_attention_forward_paged_torch,

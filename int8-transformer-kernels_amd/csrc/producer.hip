@@ -1,0 +1,186 @@
+// producer.hip — quantize-on-emit kernels for the ops that feed the INT8 attention and MLP.
+//
+// In the reference's transformer block every INT8 kernel input is produced by a
+// separate eager quantization after the fp16 producer (bench/bench_block.py:59-63,
+// 104-110, 119-121, 138-139): LayerNorm -> fp16 -> per-token quant for the MLP
+// input, and QKV projection -> split heads -> .contiguous() -> per-token quant of
+// Q, K and V.  These kernels do each of those chains in one pass:
+//
+//   layernorm_quant_kernel : y = LN(x) [fp32, biased variance, eps inside the
+//       rsqrt, optional affine], rounded to the input dtype (what F.layer_norm
+//       returns), then the per-token quantizer on that rounded y.  Optionally y
+//       itself is written too.
+//   quant_heads_kernel     : x [B, S, parts, H, Dh] (the QKV projection output
+//       viewed by part and head) -> for each part, int8 [B, H, S, Dh] and fp32
+//       scales [B, H, S]: per-token quantization over Dh, the layout the attention
+//       kernels read.
+//
+// The quantizer is the one of quant.hip: s = max(amax, 1e-8) / 127,
+// q = rn(clamp(y / s, -128, 127)) with a true division.
+#include "int8k_common.h"
+
+namespace int8k {
+namespace {
+
+__device__ __forceinline__ float load_any(const void* p, size_t i, int dtype) {
+    switch (dtype) {
+        case INT8K_DTYPE_F16: return __half2float(reinterpret_cast<const __half*>(p)[i]);
+        case INT8K_DTYPE_BF16:
+            return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+        default: return reinterpret_cast<const float*>(p)[i];
+    }
+}
+
+// Rounds an fp32 value to the storage dtype and back (what a tensor of that
+// dtype would hold), and stores it.
+__device__ __forceinline__ float round_to(float v, int dtype) {
+    switch (dtype) {
+        case INT8K_DTYPE_F16: return __half2float(__float2half_rn(v));
+        case INT8K_DTYPE_BF16: {
+            // round to nearest even on the upper 16 bits (finite inputs)
+            const uint32_t u = __float_as_uint(v);
+            const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+            return __uint_as_float(r);
+        }
+        default: return v;
+    }
+}
+
+__device__ __forceinline__ void store_any(void* p, size_t i, float v, int dtype) {
+    switch (dtype) {
+        case INT8K_DTYPE_F16: reinterpret_cast<__half*>(p)[i] = __float2half_rn(v); break;
+        case INT8K_DTYPE_BF16:
+            reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)(__float_as_uint(v) >> 16);
+            break;
+        default: reinterpret_cast<float*>(p)[i] = v;
+    }
+}
+
+__device__ __forceinline__ int8_t quantize(float y, float s) {
+    return (int8_t)(int)__builtin_rintf(fminf(fmaxf(y / s, -128.f), 127.f));
+}
+
+constexpr int kWaves = 4;
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = op(v, __shfl_xor(v, off));
+    return v;
+}
+
+// One block of 4 waves per row.  Pass 1: mean; pass 2: centred sum of squares;
+// pass 3: y and its absmax; pass 4: y again (bit-identical) and its codes.  The
+// row is re-read from L2/L1 after the first pass.
+__global__ __launch_bounds__(256) void layernorm_quant_kernel(
+    const void* __restrict__ x, int dtype, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, int8_t* __restrict__ q, float* __restrict__ scales,
+    void* __restrict__ y_out, int cols) {
+    __shared__ float red[kWaves];
+    const size_t row = blockIdx.x;
+    const size_t base = row * (size_t)cols;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    auto block_reduce = [&](float v, auto op) {
+        v = wave_reduce(v, op);
+        if (lane == 0) red[wave] = v;
+        __syncthreads();
+        float r = red[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) r = op(r, red[w]);
+        __syncthreads();
+        return r;
+    };
+    auto add = [](float a, float b) { return a + b; };
+    auto mx = [](float a, float b) { return fmaxf(a, b); };
+
+    float s = 0.f;
+    for (int c = t; c < cols; c += 256) s += load_any(x, base + c, dtype);
+    const float mean = block_reduce(s, add) / (float)cols;
+    float v = 0.f;
+    for (int c = t; c < cols; c += 256) {
+        const float d = load_any(x, base + c, dtype) - mean;
+        v = fmaf(d, d, v);
+    }
+    const float rstd = 1.f / sqrtf(block_reduce(v, add) / (float)cols + eps);
+    auto ln = [&](int c) {
+        float y = (load_any(x, base + c, dtype) - mean) * rstd;
+        if (gamma) y *= gamma[c];
+        if (beta) y += beta[c];
+        return round_to(y, dtype);
+    };
+    float m = 0.f;
+    for (int c = t; c < cols; c += 256) m = fmaxf(m, fabsf(ln(c)));
+    const float sc = fmaxf(block_reduce(m, mx), 1e-8f) / 127.f;
+    for (int c = t; c < cols; c += 256) {
+        const float y = ln(c);
+        q[base + c] = quantize(y, sc);
+        if (y_out) store_any(y_out, base + c, y, dtype);
+    }
+    if (t == 0) scales[row] = sc;
+}
+
+// One wave per source row (b, s, part, h) of Dh elements.
+__global__ __launch_bounds__(256) void quant_heads_kernel(
+    const void* __restrict__ x, int dtype, int8_t* __restrict__ q0, float* __restrict__ s0,
+    int8_t* __restrict__ q1, float* __restrict__ s1, int8_t* __restrict__ q2,
+    float* __restrict__ s2, long long rows, int S, int parts, int H, int Dh) {
+    const long long r = (long long)blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    // r = ((b * S + s) * parts + p) * H + h
+    const int h = (int)(r % H);
+    const long long r1 = r / H;
+    const int p = (int)(r1 % parts);
+    const long long bs = r1 / parts;
+    const long long b = bs / S, s = bs - b * S;
+    const size_t src = (size_t)r * Dh;
+    float m = 0.f;
+    for (int c = lane; c < Dh; c += 64) m = fmaxf(m, fabsf(load_any(x, src + c, dtype)));
+    m = wave_reduce(m, [](float a, float bb) { return fmaxf(a, bb); });
+    const float sc = fmaxf(m, 1e-8f) / 127.f;
+    int8_t* q = p == 0 ? q0 : (p == 1 ? q1 : q2);
+    float* sp = p == 0 ? s0 : (p == 1 ? s1 : s2);
+    const size_t drow = ((size_t)b * H + h) * S + s;  // [B, H, S] row of the part
+    for (int c = lane; c < Dh; c += 64) q[drow * Dh + c] = quantize(load_any(x, src + c, dtype), sc);
+    if (lane == 0) sp[drow] = sc;
+}
+
+}  // namespace
+}  // namespace int8k
+
+using namespace int8k;
+
+extern "C" int int8k_layernorm_quantize_per_token(const void* x, int dtype, const float* gamma,
+                                                  const float* beta, float eps, int8_t* q,
+                                                  float* scales, void* y_out, long long rows,
+                                                  int cols, void* stream) {
+    clear_last_error();
+    if (!x || !q || !scales || rows < 0 || cols <= 0 || !(eps >= 0.f))
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (rows >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    if (rows == 0) return INT8K_OK;
+    layernorm_quant_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+        x, dtype, gamma, beta, eps, q, scales, y_out, cols);
+    return check_launch("layernorm_quant_kernel");
+}
+
+extern "C" int int8k_quantize_heads(const void* x, int dtype, int parts, int8_t* q0, float* s0,
+                                    int8_t* q1, float* s1, int8_t* q2, float* s2, int B, int S,
+                                    int H, int head_dim, void* stream) {
+    clear_last_error();
+    if (!x || parts < 1 || parts > 3 || B <= 0 || S <= 0 || H <= 0 || head_dim <= 0)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    int8_t* qs[3] = {q0, q1, q2};
+    float* ss[3] = {s0, s1, s2};
+    for (int p = 0; p < parts; ++p)
+        if (!qs[p] || !ss[p]) return INT8K_ERR_INVALID_ARGUMENT;
+    const long long rows = (long long)B * S * parts * H;
+    if (ceil_div(rows, kWaves) >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    quant_heads_kernel<<<(unsigned)ceil_div(rows, kWaves), 256, 0, as_stream(stream)>>>(
+        x, dtype, q0, s0, q1, s1, q2, s2, rows, S, parts, H, head_dim);
+    return check_launch("quant_heads_kernel");
+}

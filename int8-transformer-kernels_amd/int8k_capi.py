@@ -51,6 +51,8 @@ _SIGNATURES = {
     "int8k_quantize_per_token": (_I, [_P, _I, _P, _P, _LL, _I, _P]),
     "int8k_kv_cache_append": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "int8k_decode_attention_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "int8k_layernorm_quantize_per_token": (_I, [_P, _I, _P, _P, _F, _P, _P, _P, _LL, _I, _P]),
+    "int8k_quantize_heads": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "int8k_decode_attention_forward_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                                   _I, _I, _I, _I, _I, _P, _SZ, _P]),
 }
@@ -319,3 +321,51 @@ def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_t
         max_pages, max_context, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
     check("int8k_decode_attention_forward_paged", st)
     return out
+
+
+def _dtype_code(t):
+    import torch
+
+    codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+    if t.dtype not in codes:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    return codes[t.dtype]
+
+
+def layernorm_quantize_per_token(x, gamma=None, beta=None, eps=1e-5, want_y=False):
+    """LN over the last dim then per-token int8: returns (q, scales[, y])."""
+    import torch
+
+    x = x.contiguous()
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    y = torch.empty_like(x) if want_y else None
+    g = gamma.float().contiguous() if gamma is not None else None
+    b = beta.float().contiguous() if beta is not None else None
+    st = load().int8k_layernorm_quantize_per_token(
+        _ptr(x), _dtype_code(x), _ptr(g) if g is not None else None,
+        _ptr(b) if b is not None else None, eps, _ptr(q), _ptr(s),
+        _ptr(y) if y is not None else None, rows, cols, _stream(x))
+    check("int8k_layernorm_quantize_per_token", st)
+    return (q, s, y) if want_y else (q, s)
+
+
+def quantize_heads(x, heads, parts=3):
+    """x [B, S, parts*heads*Dh] -> list of (q [B,H,S,Dh] int8, s [B,H,S] fp32) per part."""
+    import torch
+
+    x = x.contiguous()
+    B, S, W = x.shape
+    Dh = W // (parts * heads)
+    outs = [(torch.empty((B, heads, S, Dh), dtype=torch.int8, device=x.device),
+             torch.empty((B, heads, S), dtype=torch.float32, device=x.device))
+            for _ in range(parts)]
+    ptrs = []
+    for p in range(3):
+        ptrs += [_ptr(outs[p][0]), _ptr(outs[p][1])] if p < parts else [None, None]
+    st = load().int8k_quantize_heads(_ptr(x), _dtype_code(x), parts, *ptrs, B, S, heads, Dh,
+                                     _stream(x))
+    check("int8k_quantize_heads", st)
+    return outs

@@ -26,6 +26,10 @@ How each function is pinned (tests/test_oracle.py):
   mlp_forward : stage-by-stage against the pieces above on small shapes plus
       KATs (zero input -> zero output codes; constant input -> one code).
   quantize_fp16_per_tensor / dequantize_int8_to_fp16 : closed form + KATs.
+  layernorm_quantize_per_token : torch.nn.functional.layer_norm (an independent
+      library routine) on the same inputs, then quantize_per_token; closed
+      form for a two-valued row (y = +-1 -> codes +-127).
+  quantize_heads : a pure-Python loop over (b, s, part, h) rows on small shapes.
   gather_paged_kv / decode_attention_paged : identity block tables over a
       contiguous cache reproduce decode_attention exactly; a permuted table
       with permuted pages gives the same result; positions past a sequence's
@@ -323,3 +327,44 @@ def quantize_fp16_per_tensor(x16):
 def dequantize_int8_to_fp16(q, scale):
     """half(q * scale): kernels/quant_utils.cu:44-49, 72-77."""
     return (np.asarray(q, F32) * F32(scale)).astype(F16)
+
+
+def _round_to(y, dtype):
+    """Round float values to the storage dtype ("f16", "bf16", "f32") and back to float32."""
+    y = np.asarray(y, np.float32)
+    if dtype == "f16":
+        return y.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        u = y.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+        return r.view(np.float32)
+    return y
+
+
+def layernorm_quantize_per_token(x, gamma=None, beta=None, eps=1e-5, dtype="f16"):
+    """LayerNorm over the last dim (float64 statistics, biased variance, eps inside the
+    sqrt, optional affine), rounded to `dtype` as F.layer_norm's output would be, then
+    quantize_per_token.  Producer fusion of the reference block's LN -> _q_per_token
+    (bench/bench_block.py:59-63, 94-95, 119-121).  Returns (q int8, scales fp32, y fp32)."""
+    x = np.asarray(x, np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps)
+    if gamma is not None:
+        y = y * np.asarray(gamma, np.float64)
+    if beta is not None:
+        y = y + np.asarray(beta, np.float64)
+    y = _round_to(y.astype(np.float32), dtype)
+    q, s = quantize_per_token(y)
+    return q, s, y
+
+
+def quantize_heads(x, heads, parts=3):
+    """x [B, S, parts*heads*Dh] -> per part (q [B, H, S, Dh] int8, s [B, H, S] fp32): the
+    reference block's split_heads + .contiguous() + _q_per_token on Q, K and V
+    (bench/bench_block.py:97-102, 119-120)."""
+    x = np.asarray(x, np.float32)
+    B, S, W = x.shape
+    Dh = W // (parts * heads)
+    v = x.reshape(B, S, parts, heads, Dh).transpose(2, 0, 3, 1, 4)  # [P, B, H, S, Dh]
+    return [quantize_per_token(np.ascontiguousarray(v[p])) for p in range(parts)]

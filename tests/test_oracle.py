@@ -336,3 +336,39 @@ def test_paged_decode_identity_tables_equal_contiguous():
     np.testing.assert_array_equal(a, b_)
     ref3 = O.decode_attention(Q[1], K[1, :, :33], V[1, :, :33], sQ[1], sK[1, :, :33], sV[1, :, :33])
     np.testing.assert_allclose(a[1], ref3, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_layernorm_quantize_matches_torch_layer_norm(affine):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((33, 257)) * 3 + 1.5).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, 257).astype(np.float32) if affine else None
+    b = rng.uniform(-0.2, 0.2, 257).astype(np.float32) if affine else None
+    q, s, y = O.layernorm_quantize_per_token(x, g, b, 1e-5, "f32")
+    ref = torch.nn.functional.layer_norm(
+        torch.from_numpy(x).double(), (257,),
+        torch.from_numpy(g).double() if affine else None,
+        torch.from_numpy(b).double() if affine else None, 1e-5).float().numpy()
+    np.testing.assert_allclose(y, ref, rtol=0, atol=2e-6)
+    rq, rs = O.quantize_per_token(ref)
+    assert np.abs(q.astype(np.int32) - rq).max() <= 1
+    np.testing.assert_allclose(s, rs, rtol=1e-6)
+    # two-valued row: y = +-1 exactly -> codes +-127, scale 1/127
+    q2, s2, y2 = O.layernorm_quantize_per_token(np.array([[3.0, 5.0] * 8]), None, None, 0.0, "f16")
+    assert set(q2[0].tolist()) == {127, -127} and s2[0] == np.float32(np.float32(1.0) / 127)
+
+
+def test_quantize_heads_matches_loop():
+    rng = np.random.default_rng(8)
+    B, S, P, H, Dh = 2, 3, 3, 2, 8
+    x = rng.standard_normal((B, S, P * H * Dh)).astype(np.float32)
+    outs = O.quantize_heads(x, H, P)
+    for p in range(P):
+        for b in range(B):
+            for s in range(S):
+                for h in range(H):
+                    row = x[b, s, (p * H + h) * Dh:(p * H + h + 1) * Dh]
+                    rq, rs = O.quantize_per_token(row[None])
+                    np.testing.assert_array_equal(outs[p][0][b, h, s], rq[0])
+                    assert outs[p][1][b, h, s] == rs[0]
