@@ -520,12 +520,128 @@ def bench_gemm(args):
     }
 
 
+def bench_block(args):
+    """End-to-end pre-LN transformer block, INT8 vs FP16 (the reference's bench/bench_block.py:
+    h = x + Wo.Attn(split_heads(LN1(x).Wqkv)); y = h + MLP(LN2(h))).  The INT8 block runs
+    the attention core and the MLP on this library, with its producer-fused quantizers
+    (split-heads+quant of the QKV projection, LN2+quant of the MLP input); LayerNorm1, the
+    QKV/output projections and the residual adds stay FP16 in both paths, as in the reference.
+    Reports ms per block forward for both paths, the speedup and the cosine of the outputs."""
+    import torch
+    import torch.nn.functional as F
+
+    import int8_ext as ext
+    import workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    class Block:
+        def __init__(self, d, H, dff):
+            self.d, self.H, self.Dh, self.dff = d, H, d // H, dff
+            g = torch.Generator(device=dev).manual_seed(0)
+            rn = lambda *sh: torch.randn(*sh, generator=g, device=dev, dtype=torch.float16)  # noqa: E731
+            self.Wqkv = rn(d, 3 * d) * (d ** -0.5)
+            self.Wo = rn(d, d) * (d ** -0.5)
+            self.W1 = rn(d, dff) * (d ** -0.5)
+            self.W2 = rn(dff, d) * (dff ** -0.5)
+            w1i, self.sW1 = workloads.quantize_per_channel_w(self.W1)
+            w2i, self.sW2 = workloads.quantize_per_channel_w(self.W2)
+            self.W1T, self.W2T = ext.transpose_int8_weights(w1i, w2i)
+
+        def mlp_int8(self, h):
+            B, S, d = h.shape
+            xi, sx = ext.layernorm_quantize_per_token(h)
+            o, so = ext.int8_mlp_forward_prepacked(xi.view(B, S, d), self.W1T, self.W2T,
+                                                   sx.reshape(-1), self.sW1, self.sW2)
+            return (o.float().reshape(B, S, d) * so.reshape(B, S, 1)).half()
+
+        def mlp_fp16(self, h):
+            return F.gelu(F.layer_norm(h, (self.d,)) @ self.W1, approximate="tanh") @ self.W2
+
+        def prefill(self, x, int8):
+            B, S, _ = x.shape
+            qkv = F.layer_norm(x, (self.d,)) @ self.Wqkv
+            if int8:
+                qi, sq, ki, sk, vi, sv = ext.quantize_heads(qkv, self.H)
+                a = ext.int8_attention_forward(qi, ki, vi, sq, sk, sv)
+            else:
+                q, k, v = (t.view(B, S, self.H, self.Dh).transpose(1, 2).contiguous()
+                           for t in qkv.split(self.d, dim=-1))
+                a = F.scaled_dot_product_attention(q, k, v)
+            h = x + a.transpose(1, 2).contiguous().view(B, S, self.d) @ self.Wo
+            return h + (self.mlp_int8(h) if int8 else self.mlp_fp16(h))
+
+        def decode(self, x, kv, int8):
+            B = x.size(0)
+            q = (F.layer_norm(x, (self.d,)) @ self.Wqkv)[..., :self.d]
+            if int8:
+                Ki, Vi, sK, sV = kv
+                qi, sq = ext.quantize_per_token(q.reshape(B, self.H, self.Dh))
+                a = ext.int8_decode_attention_forward(qi, Ki, Vi, sq, sK, sV).view(B, 1, self.d)
+            else:
+                Kf, Vf = kv
+                a = F.scaled_dot_product_attention(q.view(B, self.H, 1, self.Dh), Kf, Vf)
+                a = a.transpose(1, 2).contiguous().view(B, 1, self.d)
+            h = x + a @ self.Wo
+            return h + (self.mlp_int8(h) if int8 else self.mlp_fp16(h))
+
+    def cos(a, b):
+        return F.cosine_similarity(a.float().flatten(), b.float().flatten(), dim=0).item()
+
+    rows = []
+    H, Dh, dff = 16, 64, 4096
+    d = H * Dh
+    blk = Block(d, H, dff)
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    for S in (512, 1024, 2048):
+        x = torch.randn(8, S, d, generator=g, device=dev, dtype=torch.float16)
+        c = cos(blk.prefill(x, True), blk.prefill(x, False))
+        ms8 = time_steps(lambda: blk.prefill(x, True), args.steps, args.warmup, stream)
+        ms16 = time_steps(lambda: blk.prefill(x, False), args.steps, args.warmup, stream)
+        rows.append({"regime": "prefill", "B": 8, "seq": S, "int8_ms": round(ms8, 4),
+                     "fp16_ms": round(ms16, 4), "speedup": round(ms16 / ms8, 3),
+                     "cos": round(c, 5)})
+        log(f"[bench] block prefill B8 S{S}: int8 {ms8:.3f} ms fp16 {ms16:.3f} ms "
+            f"speedup {ms16 / ms8:.2f}x cos {c:.5f}")
+    B = 128
+    x = torch.randn(B, 1, d, generator=g, device=dev, dtype=torch.float16)
+    for Skv in (2048, 4096, 8192, 16384, 32768):
+        Kf = torch.randn(B, H, Skv, Dh, generator=g, device=dev, dtype=torch.float16)
+        Vf = torch.randn(B, H, Skv, Dh, generator=g, device=dev, dtype=torch.float16)
+        Ki, sK = ext.quantize_per_token(Kf)
+        Vi, sV = ext.quantize_per_token(Vf)
+        c = cos(blk.decode(x, (Ki, Vi, sK, sV), True), blk.decode(x, (Kf, Vf), False))
+        ms8 = time_steps(lambda: blk.decode(x, (Ki, Vi, sK, sV), True), args.steps, args.warmup,
+                         stream)
+        ms16 = time_steps(lambda: blk.decode(x, (Kf, Vf), False), args.steps, args.warmup, stream)
+        rows.append({"regime": "decode", "B": B, "seq": Skv, "int8_ms": round(ms8, 4),
+                     "fp16_ms": round(ms16, 4), "speedup": round(ms16 / ms8, 3),
+                     "cos": round(c, 5)})
+        log(f"[bench] block decode B{B} Skv{Skv}: int8 {ms8:.3f} ms fp16 {ms16:.3f} ms "
+            f"speedup {ms16 / ms8:.2f}x cos {c:.5f}")
+        del Kf, Vf, Ki, Vi, sK, sV
+        torch.cuda.empty_cache()
+    head = next(r for r in rows if r["regime"] == "decode" and r["seq"] == 8192)
+    return {
+        "metric": "transformer block INT8/FP16 speedup, decode B=128 H=16 Dh=64 d_ff=4096 Skv=8192",
+        "value": head["speedup"], "unit": "x", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["int8_ms"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations and KV, random-init weights)",
+        "config": {"workload": "pre-LN transformer block d_model=1024 H=16 d_ff=4096; prefill "
+                               "B=8 S=512..2048 and decode B=128 Skv=2K..32K", "rows": rows},
+        "roofline": None, "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode-paged", "mlp", "prefill", "gemm"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "decode-paged", "mlp", "prefill", "gemm", "block"])
     ap.add_argument("--page", type=int, default=16, help="page size for --workload decode-paged")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--heads", type=int, default=32)
@@ -549,6 +665,8 @@ def main():
         res = bench_gemm(args)
     elif args.workload == "decode-paged":
         res = bench_decode_paged(args)
+    elif args.workload == "block":
+        res = bench_block(args)
     else:
         res = bench_decode(args)
     print(json.dumps(res), flush=True)

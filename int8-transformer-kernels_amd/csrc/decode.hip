@@ -613,7 +613,7 @@ static int decode_impl(const int8_t* Q, const int8_t* K, const int8_t* V, uint16
         return INT8K_ERR_MISALIGNED;
     const SplitPlan plan = plan_splits(BH, S, head_dim, nsplit);
     const long long units = (long long)BH * plan.nsplit;
-    if (units >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    if (units >= (1LL << 26)) return INT8K_ERR_UNSUPPORTED;  // 64 work-items per unit, < 2^32
     const DecodeWorkspace w = carve(workspace, units, head_dim);
     if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
     if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;
@@ -698,7 +698,7 @@ extern "C" int int8k_decode_attention_forward_paged(
     if (BH >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
     const SplitPlan plan = plan_paged((int)BH, max_context, head_dim, nsplit);
     const long long units = BH * plan.nsplit;
-    if (units >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    if (units >= (1LL << 26)) return INT8K_ERR_UNSUPPORTED;  // 64 work-items per unit, < 2^32
     const DecodeWorkspace w = carve(workspace, units, head_dim);
     if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
     if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;

@@ -435,7 +435,8 @@ extern "C" int int8k_attention_forward(const int8_t* Q, const int8_t* K, const i
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
     const long long BH = (long long)batch * heads;
-    if (BH * ((seq_len + kQ - 1) / kQ) >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    if (BH * ((seq_len + kQ - 1) / kQ) * kThreads >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
+    if ((long long)seq_len * head_dim >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;  // buffer range
     if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) || !aligned_to(out, 8) ||
         !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
         return INT8K_ERR_MISALIGNED;

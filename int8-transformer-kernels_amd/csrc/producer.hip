@@ -17,6 +17,8 @@
 //
 // The quantizer is the one of quant.hip: s = max(amax, 1e-8) / 127,
 // q = rn(clamp(y / s, -128, 127)) with a true division.
+#include <algorithm>
+
 #include "int8k_common.h"
 
 namespace int8k {
@@ -61,6 +63,9 @@ __device__ __forceinline__ int8_t quantize(float y, float s) {
 }
 
 constexpr int kWaves = 4;
+// Row kernels launch at most this many blocks (a launch must hold fewer than 2^32
+// work-items) and stride over the remaining rows.
+constexpr long long kMaxBlocks = 1LL << 20;
 
 template <typename Op>
 __device__ __forceinline__ float wave_reduce(float v, Op op) {
@@ -75,11 +80,11 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
 __global__ __launch_bounds__(256) void layernorm_quant_kernel(
     const void* __restrict__ x, int dtype, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, int8_t* __restrict__ q, float* __restrict__ scales,
-    void* __restrict__ y_out, int cols) {
+    void* __restrict__ y_out, long long rows, int cols) {
     __shared__ float red[kWaves];
-    const size_t row = blockIdx.x;
-    const size_t base = row * (size_t)cols;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (long long row = blockIdx.x; row < rows; row += gridDim.x) {  // < 2^32 work-items/launch
+    const size_t base = (size_t)row * (size_t)cols;
     auto block_reduce = [&](float v, auto op) {
         v = wave_reduce(v, op);
         if (lane == 0) red[wave] = v;
@@ -117,32 +122,35 @@ __global__ __launch_bounds__(256) void layernorm_quant_kernel(
         if (y_out) store_any(y_out, base + c, y, dtype);
     }
     if (t == 0) scales[row] = sc;
+    }
 }
 
-// One wave per source row (b, s, part, h) of Dh elements.
+// One wave per source row (b, s, part, h) of Dh elements (grid-stride).
 __global__ __launch_bounds__(256) void quant_heads_kernel(
     const void* __restrict__ x, int dtype, int8_t* __restrict__ q0, float* __restrict__ s0,
     int8_t* __restrict__ q1, float* __restrict__ s1, int8_t* __restrict__ q2,
     float* __restrict__ s2, long long rows, int S, int parts, int H, int Dh) {
-    const long long r = (long long)blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (r >= rows) return;
     const int lane = threadIdx.x & 63;
-    // r = ((b * S + s) * parts + p) * H + h
-    const int h = (int)(r % H);
-    const long long r1 = r / H;
-    const int p = (int)(r1 % parts);
-    const long long bs = r1 / parts;
-    const long long b = bs / S, s = bs - b * S;
-    const size_t src = (size_t)r * Dh;
-    float m = 0.f;
-    for (int c = lane; c < Dh; c += 64) m = fmaxf(m, fabsf(load_any(x, src + c, dtype)));
-    m = wave_reduce(m, [](float a, float bb) { return fmaxf(a, bb); });
-    const float sc = fmaxf(m, 1e-8f) / 127.f;
-    int8_t* q = p == 0 ? q0 : (p == 1 ? q1 : q2);
-    float* sp = p == 0 ? s0 : (p == 1 ? s1 : s2);
-    const size_t drow = ((size_t)b * H + h) * S + s;  // [B, H, S] row of the part
-    for (int c = lane; c < Dh; c += 64) q[drow * Dh + c] = quantize(load_any(x, src + c, dtype), sc);
-    if (lane == 0) sp[drow] = sc;
+    for (long long r = (long long)blockIdx.x * kWaves + (threadIdx.x >> 6); r < rows;
+         r += (long long)gridDim.x * kWaves) {
+        // r = ((b * S + s) * parts + p) * H + h
+        const int h = (int)(r % H);
+        const long long r1 = r / H;
+        const int p = (int)(r1 % parts);
+        const long long bs = r1 / parts;
+        const long long b = bs / S, s = bs - b * S;
+        const size_t src = (size_t)r * Dh;
+        float m = 0.f;
+        for (int c = lane; c < Dh; c += 64) m = fmaxf(m, fabsf(load_any(x, src + c, dtype)));
+        m = wave_reduce(m, [](float a, float bb) { return fmaxf(a, bb); });
+        const float sc = fmaxf(m, 1e-8f) / 127.f;
+        int8_t* q = p == 0 ? q0 : (p == 1 ? q1 : q2);
+        float* sp = p == 0 ? s0 : (p == 1 ? s1 : s2);
+        const size_t drow = ((size_t)b * H + h) * S + s;  // [B, H, S] row of the part
+        for (int c = lane; c < Dh; c += 64)
+            q[drow * Dh + c] = quantize(load_any(x, src + c, dtype), sc);
+        if (lane == 0) sp[drow] = sc;
+    }
 }
 
 }  // namespace
@@ -159,10 +167,9 @@ extern "C" int int8k_layernorm_quantize_per_token(const void* x, int dtype, cons
         return INT8K_ERR_INVALID_ARGUMENT;
     if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
         return INT8K_ERR_INVALID_ARGUMENT;
-    if (rows >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
     if (rows == 0) return INT8K_OK;
-    layernorm_quant_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
-        x, dtype, gamma, beta, eps, q, scales, y_out, cols);
+    layernorm_quant_kernel<<<(unsigned)std::min(rows, kMaxBlocks), 256, 0, as_stream(stream)>>>(
+        x, dtype, gamma, beta, eps, q, scales, y_out, rows, cols);
     return check_launch("layernorm_quant_kernel");
 }
 
@@ -179,8 +186,8 @@ extern "C" int int8k_quantize_heads(const void* x, int dtype, int parts, int8_t*
     for (int p = 0; p < parts; ++p)
         if (!qs[p] || !ss[p]) return INT8K_ERR_INVALID_ARGUMENT;
     const long long rows = (long long)B * S * parts * H;
-    if (ceil_div(rows, kWaves) >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
-    quant_heads_kernel<<<(unsigned)ceil_div(rows, kWaves), 256, 0, as_stream(stream)>>>(
+    quant_heads_kernel<<<(unsigned)std::min(ceil_div(rows, kWaves), kMaxBlocks), 256, 0,
+                         as_stream(stream)>>>(
         x, dtype, q0, s0, q1, s1, q2, s2, rows, S, parts, H, head_dim);
     return check_launch("quant_heads_kernel");
 }

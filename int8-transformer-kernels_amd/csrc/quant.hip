@@ -11,6 +11,8 @@
 //     s_row = max(amax_row, 1e-8) / 127 ; q = rn(clamp(x / s_row, -128, 127))
 //   Division (not a reciprocal multiply) and round-half-even keep the codes
 //   bit-identical to torch's `(x.float() / s).round().clamp(-128, 127)`.
+#include <algorithm>
+
 #include "int8k_common.h"
 
 namespace int8k {
@@ -95,24 +97,29 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
                                                          int8_t* __restrict__ q,
                                                          float* __restrict__ scales,
                                                          long long rows, int cols, RowMap map) {
-    const long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= rows) return;
     const int lane = threadIdx.x & 63;
-    const size_t src = (size_t)r * cols;
-    float m = 0.f;
-    for (int c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_elem(x, src + c, dtype)));
-    m = wave_max(m);
-    const float s = fmaxf(m, 1e-8f) / 127.f;
-    const long long d = map_row(r, map);
-    int8_t* qr = q + (size_t)d * cols;
-    for (int c = lane; c < cols; c += 64) qr[c] = quant_div(load_elem(x, src + c, dtype), s);
-    if (lane == 0) scales[d] = s;
+    // grid-stride over rows: a launch holds fewer than 2^32 work-items
+    for (long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows;
+         r += (long long)gridDim.x * 4) {
+        const size_t src = (size_t)r * cols;
+        float m = 0.f;
+        for (int c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_elem(x, src + c, dtype)));
+        m = wave_max(m);
+        const float s = fmaxf(m, 1e-8f) / 127.f;
+        const long long d = map_row(r, map);
+        int8_t* qr = q + (size_t)d * cols;
+        for (int c = lane; c < cols; c += 64) qr[c] = quant_div(load_elem(x, src + c, dtype), s);
+        if (lane == 0) scales[d] = s;
+    }
 }
+
+// Row kernels launch at most this many blocks and stride over the rest.
+constexpr long long kMaxRowBlocks = 1LL << 20;
 
 int launch_quant_rows(const void* x, int dtype, int8_t* q, float* scales, long long rows,
                       int cols, const RowMap& map, hipStream_t stream) {
-    const long long blocks = (rows + 3) / 4;
-    if (blocks >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
+    const long long blocks = std::min((rows + 3) / 4, kMaxRowBlocks);
+    if (blocks <= 0) return INT8K_OK;
     quant_rows_kernel<<<(unsigned)blocks, 256, 0, stream>>>(x, dtype, q, scales, rows, cols, map);
     return check_launch("quant_rows_kernel");
 }

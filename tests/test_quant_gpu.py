@@ -112,3 +112,15 @@ def test_kv_cache_capi(gpu):
     kq, ks = O.quantize_per_token(k.cpu().numpy())
     np.testing.assert_array_equal(K[:, :, 90:].cpu().numpy(), kq)
     np.testing.assert_array_equal(sK[:, :, 90:].cpu().numpy(), ks)
+
+
+def test_quantize_per_token_beyond_2p32_work_items(ext, gpu):
+    # 2^24 + 5 rows: one wave per row would need more than 2^32 work-items in one
+    # launch; the row kernels stride over rows instead (regression test)
+    rows, cols = (1 << 24) + 5, 4
+    x = torch.randn(rows, cols, generator=torch.Generator(device=gpu).manual_seed(3), device=gpu)
+    q, s = ext.quantize_per_token(x)
+    torch.cuda.synchronize()
+    idx = torch.tensor([0, 1, rows // 2, rows - 5, rows - 1], device=gpu)
+    rq, rs = workloads.quantize_per_token(x[idx].cpu())
+    assert torch.equal(q[idx].cpu(), rq) and torch.equal(s[idx].cpu(), rs)
