@@ -76,9 +76,42 @@ struct Stage {
 // as zero, so the tile loads need no clamping; masked keys never reach the
 // output.
 struct TileSrc {
-    __amdgpu_buffer_rsrc_t k, v, s;
+    __amdgpu_buffer_rsrc_t k, s;
+    v4i v;  // V descriptor with a typed format: 8_8_8_8 SSCALED (see load_v_f16x4)
     uint32_t voff_k, voff_v, voff_s;
 };
+
+// A buffer descriptor whose loads convert: data format 8_8_8_8 with numeric
+// format SSCALED turns each byte into the float of its signed value, and the
+// d16 variant of the format load packs the four as fp16.  So V arrives as exact
+// fp16 with no VALU work.  Offsets at or past `bytes` read as zero.
+__device__ __forceinline__ v4i make_v_descriptor(const void* base, uint32_t bytes) {
+    constexpr uint32_t kDstSelXYZW = 4 | (5 << 3) | (6 << 6) | (7 << 9);
+    constexpr uint32_t kNumFormatSscaled = 3, kDataFormat8888 = 10;
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    v4i d;
+    d.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b));
+    d.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32) & 0xffffu);  // stride 0
+    d.z = __builtin_amdgcn_readfirstlane(bytes);
+    d.w = kDstSelXYZW | (kNumFormatSscaled << 12) | (kDataFormat8888 << 15);
+    return d;
+}
+
+// The LLVM intrinsic behind the typed ("format") raw buffer load, which clang
+// exposes no builtin for; declared by name so the compiler schedules it and
+// tracks its wait counts like any other load.
+typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+extern "C" __device__ v4h_t int8k_raw_buffer_load_format_v4f16(v4i rsrc, int voffset, int soffset,
+                                                              int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.format.v4f16");
+
+// Four int8 at voff + soff as four fp16, packed {b0, b1} {b2, b3}.
+__device__ __forceinline__ uint2 load_v_f16x4(const v4i& desc, uint32_t voff, uint32_t soff) {
+    const v4h_t h = int8k_raw_buffer_load_format_v4f16(desc, (int)voff, (int)soff, 0);
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    const v2u r = __builtin_bit_cast(v2u, h);
+    return make_uint2(r.x, r.y);
+}
 
 template <int D>
 __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t* Vbh,
@@ -87,7 +120,7 @@ __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     TileSrc src;
     src.k = make_buffer(Kbh, (uint32_t)S * D);
-    src.v = make_buffer(Vbh, (uint32_t)S * D);
+    src.v = make_v_descriptor(Vbh, (uint32_t)S * D);
     src.s = make_buffer(wave == 0 ? sKbh : sVbh, (uint32_t)S * 4);  // waves 0 and 1 load scales
     src.voff_k = (t / (D / 16)) * D + (t % (D / 16)) * 16;
     src.voff_v = 4 * v_key_group(t) * D + 4 * v_dim_group(t);
@@ -99,7 +132,7 @@ __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t
 template <int D>
 struct Prefetch {
     int4 k[Stage<D>::kKChunks];
-    uint32_t v[Stage<D>::kVItems][4];
+    uint2 v[Stage<D>::kVItems][4];  // key 4 kg + i, dims 4 dg .. 4 dg + 3 as fp16 pairs
     float sc;  // threads 0..63: sK of key tid; 64..127: sV of key tid-64
 };
 
@@ -119,8 +152,7 @@ __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& sr
     for (int n = 0; n < Stage<D>::kVItems; ++n)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            pf.v[n][i] = __builtin_amdgcn_raw_buffer_load_b32(src.v, src.voff_v,
-                                                              k0 * D + n * 64 + i * D, 0);
+            pf.v[n][i] = load_v_f16x4(src.v, src.voff_v, k0 * D + n * 64 + i * D);
     if (threadIdx.x < 2 * kKV)
         pf.sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.s, src.voff_s,
                                                                                k0 * 4, 0));
@@ -136,23 +168,27 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
         *reinterpret_cast<int4*>(st + row * Stage<D>::kKStride + col) = pf.k[n];
     }
     _Float16* vt = reinterpret_cast<_Float16*>(st + Stage<D>::kKBytes);
+    // fp16 pair {key a, key b} of one dim from the two keys' {d, d+1} words
+    constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;
 #pragma unroll
     for (int n = 0; n < Stage<D>::kVItems; ++n) {
         const int it = t + n * kThreads;
         const int kg = v_key_group(it), dg = v_dim_group(it);
         const int p0 = vt_pos(4 * kg);
-        uint32_t x[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = pf.v[n][i] ^ 0x80808080u;
+        const uint2* w = pf.v[n];
         // dim 4 dg + j of keys 4 kg .. 4 kg + 3 -> 4 consecutive fp16 of V^T row 4 dg + j
         *reinterpret_cast<uint2*>(vt + (4 * dg + 0) * kVtStride + p0) =
-            make_uint2(biased_bytes_to_f16x2<0>(x[0], x[1]), biased_bytes_to_f16x2<0>(x[2], x[3]));
+            make_uint2(__builtin_amdgcn_perm(w[1].x, w[0].x, kLo),
+                       __builtin_amdgcn_perm(w[3].x, w[2].x, kLo));
         *reinterpret_cast<uint2*>(vt + (4 * dg + 1) * kVtStride + p0) =
-            make_uint2(biased_bytes_to_f16x2<1>(x[0], x[1]), biased_bytes_to_f16x2<1>(x[2], x[3]));
+            make_uint2(__builtin_amdgcn_perm(w[1].x, w[0].x, kHi),
+                       __builtin_amdgcn_perm(w[3].x, w[2].x, kHi));
         *reinterpret_cast<uint2*>(vt + (4 * dg + 2) * kVtStride + p0) =
-            make_uint2(biased_bytes_to_f16x2<2>(x[0], x[1]), biased_bytes_to_f16x2<2>(x[2], x[3]));
+            make_uint2(__builtin_amdgcn_perm(w[1].y, w[0].y, kLo),
+                       __builtin_amdgcn_perm(w[3].y, w[2].y, kLo));
         *reinterpret_cast<uint2*>(vt + (4 * dg + 3) * kVtStride + p0) =
-            make_uint2(biased_bytes_to_f16x2<3>(x[0], x[1]), biased_bytes_to_f16x2<3>(x[2], x[3]));
+            make_uint2(__builtin_amdgcn_perm(w[1].y, w[0].y, kHi),
+                       __builtin_amdgcn_perm(w[3].y, w[2].y, kHi));
     }
     if (t < 2 * kKV)
         reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
