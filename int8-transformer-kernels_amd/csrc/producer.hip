@@ -20,6 +20,7 @@
 #include <algorithm>
 
 #include "int8k_common.h"
+#include "rows.h"
 
 namespace int8k {
 namespace {
@@ -66,6 +67,9 @@ constexpr int kWaves = 4;
 // Row kernels launch at most this many blocks (a launch must hold fewer than 2^32
 // work-items) and stride over the remaining rows.
 constexpr long long kMaxBlocks = 1LL << 20;
+// The vectorised kernels stride over rows from a grid of at most this many
+// blocks (about 8 resident blocks per CU of a 256-CU device, 4 rounds).
+constexpr long long kVecBlocks = 8192;
 
 template <typename Op>
 __device__ __forceinline__ float wave_reduce(float v, Op op) {
@@ -153,6 +157,172 @@ __global__ __launch_bounds__(256) void quant_heads_kernel(
     }
 }
 
+// ------------------------------------------------- vectorised paths (rows.h)
+
+// Storage bits of y (already rounded to the dtype by round_to) for one chunk.
+template <int DT>
+__device__ __forceinline__ uint4 pack_chunk(const float (&y)[Vec<DT>::W]) {
+    uint32_t d[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (DT == INT8K_DTYPE_F32) {
+            d[i] = __float_as_uint(y[i]);
+        } else if constexpr (DT == INT8K_DTYPE_F16) {
+            d[i] = (uint32_t)__half_as_ushort(__float2half_rn(y[2 * i])) |
+                   ((uint32_t)__half_as_ushort(__float2half_rn(y[2 * i + 1])) << 16);
+        } else {
+            d[i] = (__float_as_uint(y[2 * i]) >> 16) | (__float_as_uint(y[2 * i + 1]) & 0xffff0000u);
+        }
+    }
+    return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// LayerNorm + per-token quantizer with the row in registers: 1 << lg lanes per
+// row, NC 16-byte chunks per lane (chunk_slots).  One read of x; the passes of
+// the one-element-per-lane kernel above become register passes.
+template <int DT, int NC>
+__global__ __launch_bounds__(256) void layernorm_quant_vec_kernel(
+    const void* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float eps, int8_t* __restrict__ q, float* __restrict__ scales, void* __restrict__ y_out,
+    uint32_t rows, int lg, int nc) {
+    constexpr int W = Vec<DT>::W;
+    constexpr int NCMAX = chunk_slots<NC>();
+    if (NC > 0) nc = NC;
+    const int lane = threadIdx.x & 63;
+    const uint32_t rpw = 64u >> lg;
+    const uint32_t c0 = lane & ((1u << lg) - 1);
+    const uint32_t cpr = (uint32_t)nc << lg;
+    const int cols = (int)cpr * W;
+    const float inv_cols = 1.f / (float)cols;
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    auto add = [](float a, float b) { return a + b; };
+    const uint32_t nw = gridDim.x * 4;
+    for (uint32_t rb = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; rb < rows; rb += nw * rpw) {
+        const uint32_t r = rb + (lane >> lg);
+        const bool ok = r < rows;
+        const uint32_t rl = min(r, rows - 1);  // loads stay outside divergent branches
+        uint4 w[NCMAX];
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NCMAX; ++i) {
+            if (NC > 0 || i < nc) {
+                w[i] = src[(size_t)rl * cpr + ((uint32_t)i << lg) + c0];
+                float v[W];
+                unpack_chunk<DT>(w[i], v);
+#pragma unroll
+                for (int e = 0; e < W; ++e) sum += v[e];
+            }
+        }
+        const float mean = row_reduce(sum, lg, add) * inv_cols;
+#pragma unroll
+        for (int i = 0; i < NCMAX; ++i) reload_barrier(w[i]);
+        float var = 0.f;
+#pragma unroll
+        for (int i = 0; i < NCMAX; ++i) {
+            if (NC > 0 || i < nc) {
+                float v[W];
+                unpack_chunk<DT>(w[i], v);
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const float d = v[e] - mean;
+                    var = fmaf(d, d, var);
+                }
+            }
+        }
+        const float rstd = 1.f / sqrtf(row_reduce(var, lg, add) * inv_cols + eps);
+#pragma unroll
+        for (int i = 0; i < NCMAX; ++i) reload_barrier(w[i]);
+        // y, rounded to the dtype, replaces x in the chunk registers (its storage
+        // bits: unpacking them gives the rounded values back exactly).  gamma and
+        // beta are re-read per row (cache hits) instead of being hoisted out of
+        // the row loop into registers.
+        const float* g = gamma;
+        const float* bt = beta;
+        asm volatile("" : "+s"(g), "+s"(bt));
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < NCMAX; ++i) {
+            if (NC > 0 || i < nc) {
+                float y[W];
+                unpack_chunk<DT>(w[i], y);
+                const int col0 = (int)((((uint32_t)i << lg) + c0) * W);
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    float t = (y[e] - mean) * rstd;
+                    if (g) t *= g[col0 + e];
+                    if (bt) t += bt[col0 + e];
+                    y[e] = round_to(t, DT);
+                    m = fmaxf(m, fabsf(y[e]));
+                }
+                w[i] = pack_chunk<DT>(y);
+            }
+        }
+        const float sc = fmaxf(row_reduce(m, lg, [](float a, float b) { return fmaxf(a, b); }),
+                               1e-8f) / 127.f;
+        if (!ok) continue;
+        const float inv = 1.f / sc;
+#pragma unroll
+        for (int i = 0; i < NCMAX; ++i) {
+            if (NC > 0 || i < nc) {
+                float y[W];
+                unpack_chunk<DT>(w[i], y);
+                const size_t chunk = (size_t)r * cpr + ((uint32_t)i << lg) + c0;
+                store_codes<W>(y, sc, inv, q + chunk * W);
+                if (y_out) reinterpret_cast<uint4*>(y_out)[chunk] = w[i];
+            }
+        }
+        if (c0 == 0) scales[r] = sc;
+    }
+}
+
+// Split-heads + per-token quantizer: source row r = ((b S + s) parts + p) H + h
+// of Dh elements, 1 << lg lanes per row, one 16-byte chunk per lane.  Each wave
+// takes U row groups of its grid stride at a time (U loads per lane in flight).
+template <int DT, int U>
+__global__ __launch_bounds__(256) void quant_heads_vec_kernel(
+    const void* __restrict__ x, int8_t* __restrict__ q0, float* __restrict__ s0,
+    int8_t* __restrict__ q1, float* __restrict__ s1, int8_t* __restrict__ q2,
+    float* __restrict__ s2, uint32_t rows, uint32_t S, uint32_t parts, uint32_t H, int lg) {
+    constexpr int W = Vec<DT>::W;
+    const int lane = threadIdx.x & 63;
+    const uint32_t rpw = 64u >> lg;
+    const uint32_t c0 = lane & ((1u << lg) - 1);
+    const int Dh = (1 << lg) * W;
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    const uint32_t stride = gridDim.x * 4 * rpw;
+    for (uint32_t rb = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; rb < rows; rb += U * stride) {
+        uint4 w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // rows past the end load the last row (no divergent branch around the
+            // loads, so they all stay in flight) and are not stored
+            const uint32_t r = min(rb + u * stride + (lane >> lg), rows - 1);
+            w[u] = src[((size_t)r << lg) + c0];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t r = rb + u * stride + (lane >> lg);
+            float v[W];
+            unpack_chunk<DT>(w[u], v);
+            float m = 0.f;
+#pragma unroll
+            for (int e = 0; e < W; ++e) m = fmaxf(m, fabsf(v[e]));
+            m = row_reduce(m, lg, [](float a, float b) { return fmaxf(a, b); });
+            if (r >= rows) continue;
+            const float sc = fmaxf(m, 1e-8f) / 127.f;
+            const float inv = 1.f / sc;
+            const uint32_t h = r % H, r1 = r / H;
+            const uint32_t p = r1 % parts, tok = r1 / parts;
+            const uint32_t b = tok / S, s = tok - b * S;
+            const size_t drow = ((size_t)b * H + h) * S + s;  // [B, H, S] row of the part
+            int8_t* q = p == 0 ? q0 : (p == 1 ? q1 : q2);
+            float* sp = p == 0 ? s0 : (p == 1 ? s1 : s2);
+            store_codes<W>(v, sc, inv, q + drow * Dh + (size_t)c0 * W);
+            if (c0 == 0) sp[drow] = sc;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace int8k
 
@@ -168,7 +338,23 @@ extern "C" int int8k_layernorm_quantize_per_token(const void* x, int dtype, cons
     if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
         return INT8K_ERR_INVALID_ARGUMENT;
     if (rows == 0) return INT8K_OK;
-    layernorm_quant_kernel<<<(unsigned)std::min(rows, kMaxBlocks), 256, 0, as_stream(stream)>>>(
+    hipStream_t st = as_stream(stream);
+    const RowShape sh = row_shape(cols, dtype);
+    const int w = dtype == INT8K_DTYPE_F32 ? 4 : 8;
+    if (sh.ok && rows < (1LL << 31) && aligned_to(x, 16) && aligned_to(q, w) &&
+        (!y_out || aligned_to(y_out, 16))) {
+        const long long waves = ceil_div(rows, 64 >> sh.lg);
+        const unsigned blocks = (unsigned)std::min(ceil_div(waves, 4), kVecBlocks);
+        with_dtype(dtype, [&](auto dt) {
+            with_chunks(sh.nc, [&](auto ncc) {
+                layernorm_quant_vec_kernel<decltype(dt)::value, decltype(ncc)::value>
+                    <<<blocks, 256, 0, st>>>(x, gamma, beta, eps, q, scales, y_out,
+                                             (uint32_t)rows, sh.lg, sh.nc);
+            });
+        });
+        return check_launch("layernorm_quant_vec_kernel");
+    }
+    layernorm_quant_kernel<<<(unsigned)std::min(rows, kMaxBlocks), 256, 0, st>>>(
         x, dtype, gamma, beta, eps, q, scales, y_out, rows, cols);
     return check_launch("layernorm_quant_kernel");
 }
@@ -186,8 +372,23 @@ extern "C" int int8k_quantize_heads(const void* x, int dtype, int parts, int8_t*
     for (int p = 0; p < parts; ++p)
         if (!qs[p] || !ss[p]) return INT8K_ERR_INVALID_ARGUMENT;
     const long long rows = (long long)B * S * parts * H;
-    quant_heads_kernel<<<(unsigned)std::min(ceil_div(rows, kWaves), kMaxBlocks), 256, 0,
-                         as_stream(stream)>>>(
+    hipStream_t st = as_stream(stream);
+    const RowShape sh = row_shape(head_dim, dtype);
+    const int w = dtype == INT8K_DTYPE_F32 ? 4 : 8;
+    bool vec = sh.ok && sh.nc == 1 && rows < (1LL << 31) && aligned_to(x, 16);
+    for (int p = 0; p < parts; ++p) vec = vec && aligned_to(qs[p], w);
+    if (vec) {
+        constexpr int U = 4;
+        const long long waves = ceil_div(rows, 64 >> sh.lg);
+        const unsigned blocks = (unsigned)std::min(ceil_div(waves, 4 * U), kVecBlocks);
+        with_dtype(dtype, [&](auto dt) {
+            quant_heads_vec_kernel<decltype(dt)::value, U><<<blocks, 256, 0, st>>>(
+                x, q0, s0, q1, s1, q2, s2, (uint32_t)rows, (uint32_t)S, (uint32_t)parts,
+                (uint32_t)H, sh.lg);
+        });
+        return check_launch("quant_heads_vec_kernel");
+    }
+    quant_heads_kernel<<<(unsigned)std::min(ceil_div(rows, kWaves), kMaxBlocks), 256, 0, st>>>(
         x, dtype, q0, s0, q1, s1, q2, s2, rows, S, parts, H, head_dim);
     return check_launch("quant_heads_kernel");
 }

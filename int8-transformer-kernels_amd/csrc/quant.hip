@@ -14,6 +14,7 @@
 #include <algorithm>
 
 #include "int8k_common.h"
+#include "rows.h"
 
 namespace int8k {
 namespace {
@@ -79,9 +80,11 @@ __global__ __launch_bounds__(256) void dequant_f16_kernel(const int8_t* __restri
 
 // ---------------------------------------------------------------- per token
 
-// One wave per row: amax pass, then the quantize pass (the row is re-read
-// from cache).  `dst_row(r)` maps source row r to its destination row, which
-// is how the KV-cache append scatters new tokens into the cache.
+// General-shape path (row lengths the chunked kernel below cannot split, or
+// unaligned pointers): one wave per row, one element per lane; amax pass, then
+// the quantize pass (the row is re-read from cache).  `map_row(r)` maps source
+// row r to its destination row, which is how the KV-cache append scatters new
+// tokens into the cache.
 struct RowMap {
     long long rows_per_group;  // source rows per (b,h) group (1 group: all rows)
     long long dst_group_stride;  // destination rows per group (cache capacity)
@@ -113,13 +116,115 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
     }
 }
 
+// Destination of source row r for the vectorised kernel: RowMap with 32-bit
+// row arithmetic (the vectorised path requires fewer than 2^31 source rows).
+struct RowDst {
+    int8_t* q;
+    float* scales;
+    int cols;
+    uint32_t rows_per_group;
+    long long dst_group_stride, dst_offset;
+    __device__ __forceinline__ void operator()(uint32_t r, int8_t*& qrow, float*& sp) const {
+        const uint32_t g = r / rows_per_group, i = r - g * rows_per_group;
+        const long long d = (long long)g * dst_group_stride + dst_offset + i;
+        qrow = q + (size_t)d * cols;
+        sp = scales + d;
+    }
+};
+
+// Vectorised per-token quantizer (one 16-byte chunk per lane, see rows.h): the
+// row is loaded once, kept in registers for the quantize step, and written as
+// 4- or 8-byte code groups.  NC chunks per lane (chunk_slots).  Each wave takes
+// U row groups of its grid stride at a time, so short rows still keep several
+// loads per lane in flight.
+template <int DT, int NC, int U>
+__global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restrict__ x,
+                                                             uint32_t rows, int lg, int nc,
+                                                             RowDst dst) {
+    constexpr int W = Vec<DT>::W;
+    constexpr int SLOTS = chunk_slots<NC>();
+    if (NC > 0) nc = NC;
+    const int lane = threadIdx.x & 63;
+    const uint32_t rpw = 64u >> lg;  // rows per wave
+    const uint32_t c0 = lane & ((1u << lg) - 1);
+    const uint32_t cpr = (uint32_t)nc << lg;  // chunks per row
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    const uint32_t stride = gridDim.x * 4 * rpw;  // rows between a wave's row groups
+    for (uint32_t rb = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; rb < rows; rb += U * stride) {
+        uint4 w[U][SLOTS];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // rows past the end load the last row (no divergent branch around the
+            // loads, so they all stay in flight) and are not stored
+            const uint32_t r = min(rb + u * stride + (lane >> lg), rows - 1);
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i)
+                if (NC > 0 || i < nc) w[u][i] = src[(size_t)r * cpr + ((uint32_t)i << lg) + c0];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t r = rb + u * stride + (lane >> lg);
+            float m = 0.f;
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) {
+                if (NC > 0 || i < nc) {
+                    float v[W];
+                    unpack_chunk<DT>(w[u][i], v);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) m = fmaxf(m, fabsf(v[e]));
+                }
+            }
+            m = row_reduce(m, lg, [](float a, float b) { return fmaxf(a, b); });
+            const float s = fmaxf(m, 1e-8f) / 127.f;
+            const float inv = 1.f / s;
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) reload_barrier(w[u][i]);
+            if (r < rows) {
+                int8_t* qrow;
+                float* sp;
+                dst(r, qrow, sp);
+#pragma unroll
+                for (int i = 0; i < SLOTS; ++i) {
+                    if (NC > 0 || i < nc) {
+                        float v[W];
+                        unpack_chunk<DT>(w[u][i], v);
+                        store_codes<W>(v, s, inv, qrow + (size_t)(((uint32_t)i << lg) + c0) * W);
+                    }
+                }
+                if (c0 == 0) *sp = s;
+            }
+        }
+    }
+}
+
 // Row kernels launch at most this many blocks and stride over the rest.
 constexpr long long kMaxRowBlocks = 1LL << 20;
+// The vectorised kernels stride over rows from a grid of at most this many
+// blocks (about 8 resident blocks per CU of a 256-CU device, 4 rounds).
+constexpr long long kVecRowBlocks = 8192;
 
 int launch_quant_rows(const void* x, int dtype, int8_t* q, float* scales, long long rows,
                       int cols, const RowMap& map, hipStream_t stream) {
+    if (rows <= 0) return INT8K_OK;
+    const RowShape sh = row_shape(cols, dtype);
+    const int w = dtype == INT8K_DTYPE_F32 ? 4 : 8;
+    if (sh.ok && rows < (1LL << 31) && map.rows_per_group < (1LL << 31) && aligned_to(x, 16) &&
+        aligned_to(q, w)) {
+        const long long waves = ceil_div(rows, 64 >> sh.lg);
+        const RowDst dst{q, scales, cols, (uint32_t)map.rows_per_group, map.dst_group_stride,
+                         map.dst_offset};
+        with_dtype(dtype, [&](auto dt) {
+            with_chunks(sh.nc, [&](auto ncc) {
+                constexpr int DT = decltype(dt)::value, NC = decltype(ncc)::value;
+                constexpr int U = NC == 1 ? 4 : (NC == 2 ? 2 : 1);
+                const unsigned blocks = (unsigned)std::min(ceil_div(waves, 4 * U), kVecRowBlocks);
+                quant_rows_vec_kernel<DT, NC, U><<<blocks, 256, 0, stream>>>(
+                    x, (uint32_t)rows, sh.lg, sh.nc, dst);
+            });
+        });
+        return check_launch("quant_rows_vec_kernel");
+    }
     const long long blocks = std::min((rows + 3) / 4, kMaxRowBlocks);
-    if (blocks <= 0) return INT8K_OK;
     quant_rows_kernel<<<(unsigned)blocks, 256, 0, stream>>>(x, dtype, q, scales, rows, cols, map);
     return check_launch("quant_rows_kernel");
 }

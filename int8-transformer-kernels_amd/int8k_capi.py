@@ -323,15 +323,6 @@ def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_t
     return out
 
 
-def _dtype_code(t):
-    import torch
-
-    codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
-    if t.dtype not in codes:
-        raise TypeError(f"unsupported dtype {t.dtype}")
-    return codes[t.dtype]
-
-
 def layernorm_quantize_per_token(x, gamma=None, beta=None, eps=1e-5, want_y=False):
     """LN over the last dim then per-token int8: returns (q, scales[, y])."""
     import torch

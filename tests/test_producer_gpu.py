@@ -20,7 +20,10 @@ _DT = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("rows,cols", [(1, 64), (37, 1000), (256, 4096)])
+# (37, 1000) and fp32 rows of 8192 take the block-per-row kernel; the others spread a row
+# over 8..64 lanes with 1..16 chunks of 16 bytes per lane.
+@pytest.mark.parametrize("rows,cols", [(1, 64), (37, 1000), (19, 1024), (5, 3072), (256, 4096),
+                                       (3, 8192)])
 @pytest.mark.parametrize("affine", [False, True])
 def test_layernorm_quantize(gpu, dtype, rows, cols, affine):
     g = torch.Generator().manual_seed(rows + cols)
@@ -43,6 +46,20 @@ def test_layernorm_quantize(gpu, dtype, rows, cols, affine):
     np.testing.assert_allclose(s.cpu().numpy(), rs, rtol=1e-3)
 
 
+def test_layernorm_quantize_unaligned_source(gpu):
+    # a source that is not 16-byte aligned takes the block-per-row kernel
+    rows, cols = 6, 1024
+    base = torch.randn(rows * cols + 1, generator=torch.Generator().manual_seed(4)).half().to(gpu)
+    x = base[1:].view(rows, cols)
+    q, s, y = capi.layernorm_quantize_per_token(x, None, None, 1e-5, want_y=True)
+    torch.cuda.synchronize()
+    rq, rs, ry = O.layernorm_quantize_per_token(x.float().cpu().numpy(), None, None, 1e-5, "f16")
+    yd = np.abs(y.float().cpu().numpy() - ry)
+    assert np.all(yd <= 2.0 ** -10 * np.maximum(np.abs(ry), 2.0 ** -14) + 1e-7), yd.max()
+    assert np.abs(q.cpu().numpy().astype(np.int32) - rq).max() <= 1
+    np.testing.assert_allclose(s.cpu().numpy(), rs, rtol=1e-3)
+
+
 def test_layernorm_quantize_torch_op_matches_two_step(ext, gpu):
     # the reference block's LN2 -> _q_per_token (bench/bench_block.py:59-63, 94-95, 121)
     x = torch.randn(8, 128, 1024, generator=torch.Generator().manual_seed(1)).half().to(gpu)
@@ -55,8 +72,11 @@ def test_layernorm_quantize_torch_op_matches_two_step(ext, gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+# Dh 48 (and fp32 Dh 512) take the one-element-per-lane kernel, the others one 16-byte chunk
+# per lane.
 @pytest.mark.parametrize("B,S,H,Dh,parts", [(1, 1, 1, 64, 1), (2, 37, 4, 64, 3), (2, 512, 16, 128, 3),
-                                             (3, 5, 2, 128, 2)])
+                                             (3, 5, 2, 128, 2), (2, 9, 3, 48, 3), (1, 7, 2, 256, 3),
+                                             (1, 3, 1, 512, 2)])
 def test_quantize_heads(ext, gpu, dtype, B, S, H, Dh, parts):
     g = torch.Generator().manual_seed(B * S + H)
     x = (torch.randn(B, S, parts * H * Dh, generator=g) * 3).to(dtype)

@@ -15,7 +15,11 @@ from oracle import int8_oracle as O
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("shape", [(1, 1), (7, 33), (1000, 128), (3, 5, 64), (64, 4096)])
+# Row lengths for both kernels: one 16-byte chunk per lane with 1..64 lanes per row
+# ((1000, 128), (3, 5, 64), (5, 256)), several chunks per lane ((33, 1024), (3, 3072),
+# (64, 4096), (2, 8192)), and one element per lane ((1, 1), (7, 33); fp32 rows of 8192).
+@pytest.mark.parametrize("shape", [(1, 1), (7, 33), (1000, 128), (3, 5, 64), (5, 256), (33, 1024),
+                                   (3, 3072), (64, 4096), (2, 8192)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_quantize_per_token_bit_exact(ext, gpu, shape, dtype):
     g = torch.Generator().manual_seed(sum(shape))
@@ -25,6 +29,19 @@ def test_quantize_per_token_bit_exact(ext, gpu, shape, dtype):
     np.testing.assert_array_equal(q.cpu().numpy(), rq)
     np.testing.assert_array_equal(s.cpu().numpy(), rs)
     assert q.shape == x.shape and tuple(s.shape) == shape[:-1]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_quantize_per_token_unaligned_source(gpu, dtype):
+    # a source that is not 16-byte aligned takes the one-element-per-lane kernel
+    rows, cols = 9, 128
+    base = (torch.randn(rows * cols + 1, generator=torch.Generator().manual_seed(5)) * 2).to(dtype)
+    x = base.to(gpu)[1:].view(rows, cols)
+    q, s = capi.quantize_per_token(x)
+    torch.cuda.synchronize()
+    rq, rs = O.quantize_per_token(x.float().cpu().numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    np.testing.assert_array_equal(s.cpu().numpy(), rs)
 
 
 def test_quantize_per_token_kats(ext, gpu):
