@@ -236,6 +236,103 @@ def bench_decode(args):
     return res
 
 
+def bench_decode_sweep(args):
+    """BASELINE config 3 (B8 H32 D64, ctx 32K) with the ctx sweep 2K..32K at B=8, and config 1
+    (B1 H12 D64 ctx 1K).  Cases whose K+V (+ scales) are under 512 MB cycle through enough copies
+    of the cache (at least 3, 768 MB in total) that the 256 MB Infinity Cache cannot serve a step
+    from the previous one.  Each case: `--warmup` untimed steps, then 5 runs of `--steps` steps;
+    the median run's mean per step is reported, with a parity sample against the C oracle."""
+    import numpy as np
+    import torch
+
+    import int8k_capi as capi
+    import workloads
+    from oracle import oracle_c
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    cases = [(1, 12, 64, 1024, 0.0)] + [(8, 32, 64, S, 0.01) for S in (2048, 4096, 8192, 16384,
+                                                                        32768)]
+    rows, last = [], None
+    for B, H, D, S, outl in cases:
+        BH = B * H
+        case = workloads.decode_case(B, H, D, S, seed=args.seed, outlier_frac=outl, device=dev)
+        Q = case["Qi"].reshape(BH, D)
+        sQ = case["sQ"].reshape(-1)
+        kv = (case["Ki"].reshape(BH, S, D), case["Vi"].reshape(BH, S, D),
+              case["sK"].reshape(-1), case["sV"].reshape(-1))
+        kv_bytes = 2 * BH * S * D
+        total = kv_bytes + 2 * BH * S * 4
+        n_copies = 1 if total >= (512 << 20) else max(3, -(-(768 << 20) // total))
+        copies = [kv] + [tuple(t.clone() for t in kv) for _ in range(n_copies - 1)]
+        out = torch.empty((BH, D), dtype=torch.float16, device=dev)
+        ws = torch.empty(max(capi.decode_workspace_bytes(BH, S, D, 0), 1), dtype=torch.uint8,
+                         device=dev)
+        it = [0]
+
+        def step():
+            K, V, sK, sV = copies[it[0] % n_copies]
+            it[0] += 1
+            capi.decode_attention(Q, K, V, sQ, sK, sV, out=out, workspace=ws)
+
+        for _ in range(args.warmup):
+            step()
+        runs = sorted(time_steps(step, args.steps, 0, stream) for _ in range(5))
+        ms = runs[2]
+        tbs = kv_bytes / (ms * 1e-3) / 1e12
+        K, V, sK, sV = kv
+        sel = np.arange(0, BH, max(1, BH // 8))
+        step_out = out.clone()
+        capi.decode_attention(Q, K, V, sQ, sK, sV, out=step_out, workspace=ws)
+        ref = oracle_c.decode_attention(Q[sel].cpu().numpy(), K[sel].cpu().numpy(),
+                                        V[sel].cpu().numpy(), sQ[sel].cpu().numpy(),
+                                        sK.reshape(BH, S)[sel].cpu().numpy(),
+                                        sV.reshape(BH, S)[sel].cpu().numpy())
+        err = float(np.abs(step_out[sel].float().cpu().numpy() - ref).max())
+        if not (err <= 2e-2):
+            raise SystemExit(f"decode B{B} H{H} D{D} S{S} does not match the oracle ({err})")
+        row = {"B": B, "H": H, "D": D, "ctx": S, "nsplit": capi.decode_num_splits(BH, S, D, 0),
+               "us": round(ms * 1e3, 2), "TBps": round(tbs, 4),
+               "pct_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS * 100, 2),
+               "cache_copies": n_copies, "max_abs_err_sample": err}
+        rows.append(row)
+        log(f"[bench] decode B{B} H{H} D{D} ctx{S}: {ms * 1e3:.1f} us {tbs:.3f} TB/s "
+            f"({row['pct_hbm_peak']:.1f}% of 8 TB/s), {n_copies} cache copies, max_abs {err:.1e}")
+        last = (case, B, H, D, S) if S == 32768 else last
+        if (B, H, S) == (1, 12, 1024):
+            cfg1 = (case, B, H, D, S)
+        del copies, kv
+        if S != 32768:
+            del case
+        torch.cuda.empty_cache()
+    head = rows[-1]
+    achieved = head["TBps"] * 1e3
+    res = {
+        "metric": "decode attn us + effective KV-read TB/s, B=8 H=32 D=64 ctx 32K (config 3), "
+                  "ctx sweep 2K-32K and config 1",
+        "value": head["TBps"], "unit": "TB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(head["us"] / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1), 1% channels x8 (none for config 1), per-token int8)",
+        "config": {"workload": "int8-kv decode attention B=8 H=32 D=64 ctx=32768; sweep and "
+                               "config 1 in rows", "rows": rows},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("decode_b8h32d64_s32768"),
+                     "kernel": "decode_split_kernel + decode_combine_kernel (one step)"},
+    }
+    if not args.no_cpu_baseline:
+        case, B, H, D, S = cfg1
+        cb = cpu_baseline_decode(case, B, H, D, S, budget_s=args.cpu_budget)
+        log(f"[bench] cpu baseline (config 1): {cb['value'] * 1e3:.3f} GB/s on {cb['cores']} "
+            f"threads")
+        res["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    else:
+        res["cpu_baseline"] = None
+    return res
+
+
 def bench_decode_paged(args):
     """The headline decode over a paged copy of the same cache: pages of --page positions in
     a seeded random physical order, one block table row per sequence, all lengths = ctx."""
@@ -641,7 +738,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode-paged", "mlp", "prefill", "gemm", "block"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "decode-sweep", "decode-paged", "mlp", "prefill", "gemm",
+                             "block"])
     ap.add_argument("--page", type=int, default=16, help="page size for --workload decode-paged")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--heads", type=int, default=32)
@@ -665,6 +764,8 @@ def main():
         res = bench_gemm(args)
     elif args.workload == "decode-paged":
         res = bench_decode_paged(args)
+    elif args.workload == "decode-sweep":
+        res = bench_decode_sweep(args)
     elif args.workload == "block":
         res = bench_block(args)
     else:
