@@ -133,10 +133,15 @@ def cpu_baseline_decode(case, B, H, D, S, budget_s=12.0):
         heads += n
         n *= 2
     tbs = done_bytes / spent / 1e12
+    # one thread on the first head, for the per-core figure
+    args = [t[0:1].cpu().numpy() for t in (Q, K, V, sQ, sK, sV)]
+    t0 = time.perf_counter()
+    oracle_c.decode_attention(*args, threads=1)
+    one = 2 * S * D / (time.perf_counter() - t0) / 1e9
     return dict(value=tbs, unit="TB/s", cores=threads, kind="port",
                 sample=f"C oracle (float64, OpenMP) on {heads} of {BH} (b,h) heads of the "
                        f"same B{B} H{H} D{D} S{S} inputs; {spent:.1f} s of CPU time; "
-                       f"host os.cpu_count()={os.cpu_count()}",
+                       f"host os.cpu_count()={os.cpu_count()}; 1 thread: {one:.2f} GB/s",
                 seconds=spent, heads=heads)
 
 
