@@ -117,3 +117,56 @@ def test_quant_argument_validation(capi):
         _fake(0x10000), _fake(0x20000), _fake(0x30000), _fake(0x40000), _fake(0x50000),
         _fake(0x60000), _fake(0x70000), 4, 200, 100, 128, 0, _fake(0x80000), 1 << 30,
         None) == capi.INT8K_ERR_INVALID_ARGUMENT
+
+
+def test_paged_decode_argument_validation(capi):
+    lib = capi.load()
+    F = _fake
+
+    def call(page=16, max_pages=4, max_context=64, D=128, K=0x20000, ws_bytes=1 << 30):
+        return lib.int8k_decode_attention_forward_paged(
+            F(0x10000), F(K), F(0x30000), F(0x40000), F(0x50000), F(0x60000), F(0x70000),
+            F(0x80000), F(0x90000), 2, 4, D, 8, page, max_pages, max_context, 0, F(0xa0000),
+            ws_bytes, None)
+
+    assert call(page=24) == capi.INT8K_ERR_UNSUPPORTED      # not a power of two
+    assert call(page=8) == capi.INT8K_ERR_UNSUPPORTED       # below 16
+    assert call(page=2048) == capi.INT8K_ERR_UNSUPPORTED    # above 1024
+    assert call(D=96) == capi.INT8K_ERR_UNSUPPORTED
+    assert call(max_context=65) == capi.INT8K_ERR_INVALID_ARGUMENT  # > max_pages * page
+    assert call(K=0x20008) == capi.INT8K_ERR_MISALIGNED
+    need = lib.int8k_decode_attention_paged_workspace_bytes(2, 4, 64, 128, 0)
+    assert need > 0
+    assert call(ws_bytes=need - 1) == capi.INT8K_ERR_WORKSPACE
+
+
+def test_producer_argument_validation(capi):
+    lib = capi.load()
+    F = _fake
+    # LayerNorm + quantize: unknown dtype, negative eps
+    assert lib.int8k_layernorm_quantize_per_token(F(0x10000), 9, None, None, 1e-5, F(0x20000),
+                                                  F(0x30000), None, 4, 64,
+                                                  None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert lib.int8k_layernorm_quantize_per_token(F(0x10000), 0, None, None, -1.0, F(0x20000),
+                                                  F(0x30000), None, 4, 64,
+                                                  None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    # zero rows is a no-op
+    assert lib.int8k_layernorm_quantize_per_token(F(0x10000), 0, None, None, 1e-5, F(0x20000),
+                                                  F(0x30000), None, 0, 64, None) == capi.INT8K_OK
+    # split heads: parts out of range, a missing output of a requested part
+    assert lib.int8k_quantize_heads(F(0x10000), 0, 4, F(1), F(2), F(3), F(4), F(5), F(6), 1, 2,
+                                    2, 64, None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert lib.int8k_quantize_heads(F(0x10000), 0, 2, F(0x20000), F(0x30000), None, None, None,
+                                    None, 1, 2, 2, 64, None) == capi.INT8K_ERR_INVALID_ARGUMENT
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(repo, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
