@@ -18,6 +18,15 @@
 // — no atomics, no zero-fill), requant_rows_kernel (reduces the partials,
 // requantizes a row), tensor_absmax_kernel and transpose_i8_kernel (weight
 // packing to the K-contiguous [N][K] layout the MFMA operands want).
+//
+// Few tokens (decode-time MLPs, T = B): 256 x 256 tiles leave most CUs idle
+// (T = 128 gives 16 blocks for GEMM1 and 4 for GEMM2).  When a GEMM has fewer
+// tiles than CUs it runs split-K instead: gemm_i8_splitk_kernel (128 x 128
+// output tiles, the K range split over blocks, exact int32 partials) and
+// splitk_epilogue_kernel<EPI> (sums the partials per row, then the same
+// epilogue math as gemm_i8_kernel, writing the same fp16 output and absmax
+// partials), so requant_rows_kernel and every result are the same on both
+// paths.
 #include <algorithm>
 
 #include "gemm_i8.h"
@@ -160,6 +169,168 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     }
 }
 
+// ---------------------------------------------------------------- split-K path
+
+constexpr int kSkN = 128;       // output columns per block (4 waves x 32)
+constexpr int kSkM = 128;       // output rows per block (4 MFMA row tiles)
+constexpr int kSkK = 128;       // K bytes per step
+constexpr int kSkStride = kSkK + 16;  // padded LDS row of the A tile
+constexpr int kSkLds = 2 * kSkM * kSkStride;
+
+// P[split][M][N] (int32) = A[m0:m0+128, k range] . Bt[n0:n0+128, k range]^T.
+// grid = (N tiles, splits, M tiles); each wave owns 32 columns and all 128 rows
+// (4 x 32x32x32 MFMA tiles).  The A tile goes through LDS (shared by the four
+// waves); B fragments are loaded straight from global memory (each column is
+// used by one wave only).  K is a multiple of 32; rows >= M read as zero.
+__global__ __launch_bounds__(256) void gemm_i8_splitk_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int32_t* __restrict__ P,
+    int M, int N, int K, int k_per_split) {
+    extern __shared__ __align__(16) char lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * kSkN, m0 = blockIdx.z * kSkM;
+    const int kb = blockIdx.y * k_per_split;
+    const int ke = min(K, kb + k_per_split);
+    const int ncol = n0 + wave * 32 + (lane & 31);
+    const int8_t* brow = Bt + (size_t)min(ncol, N - 1) * K;
+    v16i acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0;
+
+    // A staging: 128 rows x 128 bytes = 1024 chunks of 16 B, 4 per thread
+    int4 ar[4];
+    auto load_a = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = threadIdx.x + i * 256;
+            const int row = c >> 3, kc = (c & 7) * 16;
+            const int gk = min(k0 + kc, K - 16);
+            ar[i] = *reinterpret_cast<const int4*>(A + (size_t)min(m0 + row, M - 1) * K + gk);
+        }
+    };
+    auto store_a = [&](char* buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = threadIdx.x + i * 256;
+            const int row = c >> 3, kc = (c & 7) * 16;
+            int4 v = ar[i];
+            if (!(m0 + row < M && k0 + kc < ke)) v = make_int4(0, 0, 0, 0);
+            *reinterpret_cast<int4*>(buf + row * kSkStride + kc) = v;
+        }
+    };
+    const int nsteps = (ke - kb + kSkK - 1) / kSkK;
+    load_a(kb);
+    for (int st = 0; st < nsteps; ++st) {
+        const int k0 = kb + st * kSkK;
+        char* buf = lds + (st & 1) * (kSkM * kSkStride);
+        store_a(buf, k0);
+        // B fragments of this step: column ncol, bytes k0 + 32 s + 16 (lane / 32)
+        v4i bf[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kk = k0 + 32 * s + 16 * (lane >> 5);
+            bf[s] = kk < ke ? *reinterpret_cast<const v4i*>(brow + kk) : v4i{0, 0, 0, 0};
+        }
+        if (st + 1 < nsteps) load_a(k0 + kSkK);
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (k0 + 32 * s >= ke) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const v4i af = *reinterpret_cast<const v4i*>(
+                    buf + (32 * i + (lane & 31)) * kSkStride + 32 * s + 16 * (lane >> 5));
+                acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[s], acc[i], 0, 0, 0);
+            }
+        }
+    }
+    if (ncol >= N) return;
+    int32_t* Pp = P + (size_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + 32 * i + acc_row(r, lane);
+            if (row < M) Pp[(size_t)row * N + ncol] = acc[i][r];
+        }
+}
+
+// acc = sum of the split partials (exact int32), then gemm_i8_kernel's
+// epilogue math for EPI (same expressions) and the fp16 store.  Block (x, y)
+// covers columns [256 x, 256 x + 256) of row y and writes that chunk's absmax
+// to pmax[x][row], like one 256-column tile of gemm_i8_kernel.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ P,
+                                                              int splits, int M, int N,
+                                                              EpiParams p) {
+    __shared__ float red[4];
+    const int row = blockIdx.y;
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    float m = 0.f;
+    if (n < N) {
+        const int32_t* col = P + (size_t)row * N + n;
+        const size_t plane = (size_t)M * N;
+        int acc = 0;
+#pragma unroll 8
+        for (int sp = 0; sp < splits; ++sp) acc += col[sp * plane];
+        float v = static_cast<float>(acc) * p.sa[(size_t)row * p.sa_stride] *
+                  p.sb[(size_t)n * p.sb_stride];
+        if constexpr (EPI == EPI_GELU_F16)
+            v = gelu_tanh(v + (p.bias != nullptr ? p.bias[n] : 0.f));
+        m = fabsf(v);
+        p.c16[(size_t)row * p.ldc + n] = f32_to_f16_bits(v);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        p.pmax[(size_t)blockIdx.x * M + row] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Split plan for an M x N x K GEMM: run split-K when the 256 x 256 grid would
+// have fewer tiles than the device has CUs (256 on MI355X).
+struct SplitKPlan {
+    bool use;
+    int splits, k_per_split, tiles_n, tiles_m;
+};
+
+inline SplitKPlan splitk_plan(int M, int N, int K) {
+    SplitKPlan pl{};
+    const long long big_tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (big_tiles >= 256 || K % 32 != 0 || M > 4 * kSkM) return pl;
+    pl.tiles_n = (N + kSkN - 1) / kSkN;
+    pl.tiles_m = (M + kSkM - 1) / kSkM;
+    const int ksteps = (K + kSkK - 1) / kSkK;
+    const int want = (int)std::max<long long>(1, (512 + pl.tiles_n * pl.tiles_m - 1) /
+                                                     (pl.tiles_n * pl.tiles_m));
+    const int steps_per = (ksteps + std::min(want, ksteps) - 1) / std::min(want, ksteps);
+    pl.k_per_split = steps_per * kSkK;
+    pl.splits = (K + pl.k_per_split - 1) / pl.k_per_split;
+    pl.use = true;
+    return pl;
+}
+
+inline size_t splitk_partial_bytes(int M, int N, int K) {
+    const SplitKPlan pl = splitk_plan(M, N, K);
+    return pl.use ? (size_t)pl.splits * M * N * 4 : 0;
+}
+
+template <int EPI>
+int launch_gemm_splitk(const int8_t* A, const int8_t* Bt, int M, int N, int K,
+                       const SplitKPlan& pl, int32_t* partial, const EpiParams& p,
+                       hipStream_t stream) {
+    const dim3 grid(pl.tiles_n, pl.splits, pl.tiles_m);
+    gemm_i8_splitk_kernel<<<grid, 256, kSkLds, stream>>>(A, Bt, partial, M, N, K,
+                                                         pl.k_per_split);
+    int st = check_launch("gemm_i8_splitk_kernel");
+    if (st != INT8K_OK) return st;
+    splitk_epilogue_kernel<EPI><<<dim3((N + 255) / 256, M), 256, 0, stream>>>(partial, pl.splits,
+                                                                              M, N, p);
+    return check_launch("splitk_epilogue_kernel");
+}
+
 // One block per row: reduce the row's absmax partials, then requantize the
 // fp16 row to int8 with scale max(amax,1e-8)/127 (quantize_rows semantics).
 // With `tensor_amax` set, that single value is used for every row instead
@@ -266,6 +437,7 @@ struct MlpWorkspace {
     uint16_t* o16;    // [T][d_model]
     float* p2;        // [tiles_n2][T]
     float* tmax;      // [1]
+    int32_t* part;    // split-K partials (the larger GEMM's), when a GEMM runs split-K
     size_t bytes;
 };
 
@@ -288,6 +460,8 @@ MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
     w.o16 = reinterpret_cast<uint16_t*>(take((size_t)T * dm * 2));
     w.p2 = reinterpret_cast<float*>(take((size_t)((dm + BN - 1) / BN) * T * 4));
     w.tmax = reinterpret_cast<float*>(take(4));
+    w.part = reinterpret_cast<int32_t*>(take(std::max(splitk_partial_bytes(T, dff, dm),
+                                                      splitk_partial_bytes(T, dm, dff))));
     w.bytes = off;
     return w;
 }
@@ -392,8 +566,14 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p1.sb_stride = n_scale_W1 == 1 ? 0 : 1;
     p1.bias = bias1;
     p1.pmax = w.p1;
-    if ((st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s)) != INT8K_OK) return st;
-    // per-token requant of the hidden
+    const SplitKPlan sk1 = splitk_plan(T, d_ff, d_model);
+    if (sk1.use)
+        st = launch_gemm_splitk<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, sk1, w.part, p1, s);
+    else
+        st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
+    if (st != INT8K_OK) return st;
+    // per-token requant of the hidden (either path leaves one absmax partial per
+    // 256 columns and row)
     const int tn1 = (d_ff + BN - 1) / BN;
     requant_rows_kernel<<<T, 256, 0, s>>>(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T,
                                           d_ff);
@@ -407,7 +587,12 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p2.sb = scale_W2;
     p2.sb_stride = n_scale_W2 == 1 ? 0 : 1;
     p2.pmax = w.p2;
-    if ((st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s)) != INT8K_OK) return st;
+    const SplitKPlan sk2 = splitk_plan(T, d_model, d_ff);
+    if (sk2.use)
+        st = launch_gemm_splitk<EPI_F16>(w.hq, W2t, T, d_model, d_ff, sk2, w.part, p2, s);
+    else
+        st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
+    if (st != INT8K_OK) return st;
     const int tn2 = (d_model + BN - 1) / BN;
     const float* tmax = nullptr;
     if (per_tensor_out) {

@@ -91,6 +91,28 @@ def test_mlp_bias_vs_oracle(ext, gpu):
     _compare_mlp(_np(out).reshape(T, dm), _np(osc), ref, rsc, "bias")
 
 
+@pytest.mark.parametrize("T,dm,dff", [(128, 1024, 4096), (64, 512, 2048)])
+def test_mlp_few_tokens_split_k(capi_mlp, gpu, T, dm, dff):
+    # decode-time token counts: both GEMMs run split-K (fewer 256 x 256 tiles than CUs)
+    c, n = _mlp_case(T, dm, dff, seed=T + 5, gpu=gpu)
+    out, osc = capi.mlp_forward(c["x"].reshape(T, dm), c["W1"], c["W2"], c["sx"], c["sW1"],
+                                c["sW2"])
+    torch.cuda.synchronize()
+    ref, rsc = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                             n["sW2"], gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out), _np(osc), ref, rsc, f"split-K T{T}")
+    # per-tensor output scale on the same path
+    sx1 = c["sx"].reshape(-1)[:1].clone()
+    sw1 = c["sW1"].reshape(-1)[:1].clone()
+    sw2 = c["sW2"].reshape(-1)[:1].clone()
+    out_t, osc_t = capi.mlp_forward(c["x"].reshape(T, dm), c["W1"], c["W2"], sx1, sw1, sw2,
+                                    flags=capi.MLP_OUT_PER_TENSOR)
+    torch.cuda.synchronize()
+    ref_t, rsc_t = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], _np(sx1), _np(sw1),
+                                 _np(sw2), per_token_out=False, gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out_t), _np(osc_t), ref_t, rsc_t, f"split-K per-tensor T{T}")
+
+
 def test_mlp_per_tensor_reference_config(ext, gpu):
     # tests/test_int8.py:130-154: batch 2, seq 512, 512 -> 2048, per-tensor scales
     g = torch.Generator().manual_seed(42)
