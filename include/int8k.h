@@ -222,6 +222,18 @@ int int8k_dequantize_int8_to_fp16(const int8_t* input, uint16_t* output, float s
 int int8k_quantize_per_token(const void* x, int dtype, int8_t* q, float* scales,
                              long long rows, int cols, void* stream);
 
+/* Per-token (row) dequantization of q [rows, cols] int8 with scales [rows]
+ * into y [rows, cols] of `dtype`: y = T(float(q) * s_row), T the rounding to
+ * the dtype applied to the fp32 product (PyTorch's
+ * `(q.float() * s[:, None]).to(dtype)`, two roundings); with a non-NULL
+ * residual [rows, cols] of the same dtype, y = T(float(residual) + that) (the
+ * residual add of a transformer block).  The consumer side of the INT8 MLP
+ * output (int8 + per-token scale).  No counterpart in the reference (its
+ * callers dequantize in PyTorch, bench/bench_block.py:113, 126-127). */
+int int8k_dequantize_per_token(const int8_t* q, const float* scales, int dtype,
+                               const void* residual, void* y, long long rows, int cols,
+                               void* stream);
+
 /* INT8 KV-cache append: quantizes n_new tokens per (b,h) of k_new/v_new
  * [BH, n_new, head_dim] (fp16, bf16 or fp32) per token into rows
  * pos .. pos+n_new-1 of K_cache/V_cache [BH, capacity, head_dim] and their

@@ -408,6 +408,41 @@ std::tuple<torch::Tensor, torch::Tensor> quantize_per_token_torch(torch::Tensor 
     return {q, s};
 }
 
+// Per-token dequantization: y = (q.float() * s[..., None]).to(dtype), or with a
+// residual r: r + that (in r's dtype, which then sets the output dtype).
+torch::Tensor dequantize_per_token_torch(torch::Tensor q, torch::Tensor s,
+                                         c10::optional<torch::Tensor> residual,
+                                         c10::optional<at::ScalarType> dtype) {
+    TORCH_CHECK(q.device().is_cuda(), "q must be a CUDA tensor");
+    TORCH_CHECK(q.dtype() == torch::kInt8, "q must be int8");
+    TORCH_CHECK(q.dim() >= 1 && q.numel() > 0, "q must be a non-empty tensor");
+    const int64_t cols = q.size(-1);
+    TORCH_CHECK(cols <= INT32_MAX, "rows too long");
+    const int64_t rows = q.numel() / cols;
+    TORCH_CHECK(s.numel() == rows, "scales must have one element per row of q");
+    TORCH_CHECK(s.device() == q.device(), "scales must be on q's device");
+    torch::ScalarType out_t = torch::kFloat16;
+    torch::Tensor r;
+    if (residual.has_value() && residual->defined()) {
+        r = residual->contiguous();
+        TORCH_CHECK(r.sizes() == q.sizes(), "residual must have q's shape");
+        TORCH_CHECK(r.device() == q.device(), "residual must be on q's device");
+        out_t = r.scalar_type();
+    } else if (dtype.has_value()) {
+        out_t = *dtype;
+    }
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+    auto y = torch::empty(q.sizes(), torch::TensorOptions().dtype(out_t).device(q.device()));
+    const int code = dtype_code(y);
+    auto qc = q.contiguous();
+    auto sc = s.to(torch::kFloat32).contiguous();
+    check_status(int8k_dequantize_per_token(qc.data_ptr<int8_t>(), sc.data_ptr<float>(), code,
+                                            r.defined() ? r.data_ptr() : nullptr, y.data_ptr(),
+                                            rows, (int)cols, current_stream(q)),
+                 "dequantize_per_token");
+    return y;
+}
+
 // LayerNorm over the last dim, rounded to x's dtype, then per-token int8:
 // returns (q, scales).  weight/bias optional (any float dtype; used as fp32).
 std::tuple<torch::Tensor, torch::Tensor> layernorm_quantize_per_token_torch(
@@ -631,6 +666,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "int8 -> fp16 with a scalar scale");
     m.def("quantize_per_token", &quantize_per_token_torch,
           "Per-token (last dim) int8 quantization — returns (int8, fp32 scales)");
+    m.def("dequantize_per_token", &dequantize_per_token_torch,
+          "Per-token int8 -> float (q * s[..., None]) rounded to dtype, plus an optional "
+          "residual (whose dtype then sets the output's)",
+          py::arg("q"), py::arg("scales"), py::arg("residual") = py::none(),
+          py::arg("dtype") = py::none());
     m.def("layernorm_quantize_per_token", &layernorm_quantize_per_token_torch,
           "LayerNorm (last dim) then per-token int8 — returns (int8, fp32 scales)",
           py::arg("x"), py::arg("weight") = py::none(), py::arg("bias") = py::none(),

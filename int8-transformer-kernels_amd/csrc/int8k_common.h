@@ -106,6 +106,16 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
     return __half_as_ushort(__float2half_rn(x));
 }
 
+// fp32 -> fp16 (round to nearest even) of x as an fp32 number.  clang folds
+// half(a * b) into v_fma_mixlo_f16, which rounds the exact product to fp16 in
+// one step; PyTorch's (q.float() * s).half() rounds it to fp32 first, and the
+// two differ when that first rounding lands on an fp16 tie.  The empty asm
+// pins x as the fp32 value, for outputs that must match bit for bit.
+__device__ __forceinline__ __half f16_of_f32(float x) {
+    asm volatile("" : "+v"(x));
+    return __float2half_rn(x);
+}
+
 // Raw buffer resource over [base, base + bytes): loads at offsets past the end
 // return zero, so tiles that overhang a matrix need no clamped addresses.  The
 // arguments must be the same for the whole wave (they go to scalar registers).

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void dequant_f16_kernel(const int8_t* __restri
                                                           __half* __restrict__ y, size_t n,
                                                           float scale) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
-        y[i] = __float2half_rn((float)q[i] * scale);
+        y[i] = f16_of_f32((float)q[i] * scale);
 }
 
 // ---------------------------------------------------------------- per token
@@ -197,6 +197,95 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restr
     }
 }
 
+// Per-token dequantization, the consumer side of the INT8 MLP / attention
+// outputs: y[r, c] = T(float(q[r, c]) * s[r]) with T the rounding to the output
+// dtype, and, with a residual, y = T(float(res[r, c]) + float(that)) — the
+// values of PyTorch's `(q.float() * s[:, None]).to(dtype)` and of
+// `res + that` in the residual's dtype.  The product is rounded to fp32 and
+// then to the output dtype, and the add rounds again: FP contraction is off in
+// these kernels (an FMA would round once for fp32) and f16_of_f32 keeps the
+// fp16 conversion from fusing into the multiply.  16 codes per lane
+// (cols % 16 == 0); the general path is one element per thread.
+template <int DT>
+__device__ __forceinline__ float round_dtype(float v) {
+    if constexpr (DT == INT8K_DTYPE_F16) return __half2float(f16_of_f32(v));
+    else if constexpr (DT == INT8K_DTYPE_BF16) {
+        const uint32_t u = __float_as_uint(v);
+        return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+    } else return v;
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t dtype_bits16(float v) {  // v already rounded
+    if constexpr (DT == INT8K_DTYPE_F16) return __half_as_ushort(__float2half_rn(v));
+    else return __float_as_uint(v) >> 16;
+}
+
+template <int DT>
+__device__ __forceinline__ float load_dtype(const void* p, size_t i) {
+    if constexpr (DT == INT8K_DTYPE_F16)
+        return __half2float(reinterpret_cast<const __half*>(p)[i]);
+    else if constexpr (DT == INT8K_DTYPE_BF16)
+        return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+    else return reinterpret_cast<const float*>(p)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void store_dtype(void* p, size_t i, float v) {
+    if constexpr (DT == INT8K_DTYPE_F32) reinterpret_cast<float*>(p)[i] = v;
+    else reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)dtype_bits16<DT>(v);
+}
+
+template <int DT, bool RES>
+__global__ __launch_bounds__(256) void dequant_rows_vec_kernel(const int8_t* __restrict__ q,
+                                                               const float* __restrict__ sc,
+                                                               const void* __restrict__ res,
+                                                               void* __restrict__ y,
+                                                               uint32_t chunks, uint32_t cpr) {
+#pragma clang fp contract(off)
+    for (uint32_t g = blockIdx.x * 256 + threadIdx.x; g < chunks; g += gridDim.x * 256) {
+        const uint4 w = reinterpret_cast<const uint4*>(q)[g];
+        const float s = sc[g / cpr];
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            v[i] = round_dtype<DT>((float)(int8_t)(wd[i >> 2] >> (8 * (i & 3))) * s);
+        if constexpr (RES) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                v[i] = round_dtype<DT>(load_dtype<DT>(res, (size_t)g * 16 + i) + v[i]);
+        }
+        if constexpr (DT == INT8K_DTYPE_F32) {
+            float4* o = reinterpret_cast<float4*>(y) + (size_t)g * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+        } else {
+            uint32_t b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                b[j] = dtype_bits16<DT>(v[2 * j]) | (dtype_bits16<DT>(v[2 * j + 1]) << 16);
+            uint4* o = reinterpret_cast<uint4*>(y) + (size_t)g * 2;
+            o[0] = make_uint4(b[0], b[1], b[2], b[3]);
+            o[1] = make_uint4(b[4], b[5], b[6], b[7]);
+        }
+    }
+}
+
+template <int DT, bool RES>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q,
+                                                           const float* __restrict__ sc,
+                                                           const void* __restrict__ res,
+                                                           void* __restrict__ y, size_t n,
+                                                           int cols) {
+#pragma clang fp contract(off)
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float v = round_dtype<DT>((float)q[i] * sc[i / cols]);
+        if constexpr (RES) v = round_dtype<DT>(load_dtype<DT>(res, i) + v);
+        store_dtype<DT>(y, i, v);
+    }
+}
+
 // Row kernels launch at most this many blocks and stride over the rest.
 constexpr long long kMaxRowBlocks = 1LL << 20;
 // The vectorised kernels stride over rows from a grid of at most this many
@@ -301,4 +390,43 @@ extern "C" int int8k_kv_cache_append(const void* k_new, const void* v_new, int d
     int st = launch_quant_rows(k_new, dtype, K_cache, sK_cache, rows, head_dim, map, s);
     if (st != INT8K_OK) return st;
     return launch_quant_rows(v_new, dtype, V_cache, sV_cache, rows, head_dim, map, s);
+}
+
+extern "C" int int8k_dequantize_per_token(const int8_t* q, const float* scales, int dtype,
+                                          const void* residual, void* y, long long rows,
+                                          int cols, void* stream) {
+    clear_last_error();
+    if (!q || !scales || !y || rows < 0 || cols <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (dtype != INT8K_DTYPE_F16 && dtype != INT8K_DTYPE_BF16 && dtype != INT8K_DTYPE_F32)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    const size_t ea = dtype == INT8K_DTYPE_F32 ? 4 : 2;
+    if (!aligned_to(scales, 4) || !aligned_to(y, ea) || (residual && !aligned_to(residual, ea)))
+        return INT8K_ERR_MISALIGNED;
+    if (rows == 0) return INT8K_OK;
+    hipStream_t s = as_stream(stream);
+    const size_t n = (size_t)rows * cols;
+    const bool vec = cols % 16 == 0 && n / 16 < (1ULL << 32) && aligned_to(q, 16) &&
+                     aligned_to(y, 16) && (!residual || aligned_to(residual, 16));
+    with_dtype(dtype, [&](auto dt) {
+        constexpr int DT = decltype(dt)::value;
+        if (vec) {
+            const uint32_t chunks = (uint32_t)(n / 16);
+            const unsigned blocks = (unsigned)std::min<long long>(ceil_div(chunks, 256), 8192);
+            if (residual)
+                dequant_rows_vec_kernel<DT, true><<<blocks, 256, 0, s>>>(
+                    q, scales, residual, y, chunks, (uint32_t)(cols / 16));
+            else
+                dequant_rows_vec_kernel<DT, false><<<blocks, 256, 0, s>>>(
+                    q, scales, residual, y, chunks, (uint32_t)(cols / 16));
+        } else {
+            const unsigned blocks = (unsigned)std::min<long long>(ceil_div((long long)n, 256), 8192);
+            if (residual)
+                dequant_rows_kernel<DT, true><<<blocks, 256, 0, s>>>(q, scales, residual, y, n,
+                                                                      cols);
+            else
+                dequant_rows_kernel<DT, false><<<blocks, 256, 0, s>>>(q, scales, residual, y, n,
+                                                                       cols);
+        }
+    });
+    return check_launch(vec ? "dequant_rows_vec_kernel" : "dequant_rows_kernel");
 }

@@ -49,6 +49,7 @@ _SIGNATURES = {
     "int8k_quantize_fp16_to_int8": (_I, [_P, _P, _P, _LL, _P]),
     "int8k_dequantize_int8_to_fp16": (_I, [_P, _P, _F, _LL, _P]),
     "int8k_quantize_per_token": (_I, [_P, _I, _P, _P, _LL, _I, _P]),
+    "int8k_dequantize_per_token": (_I, [_P, _P, _I, _P, _P, _LL, _I, _P]),
     "int8k_kv_cache_append": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "int8k_decode_attention_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "int8k_layernorm_quantize_per_token": (_I, [_P, _I, _P, _P, _F, _P, _P, _P, _LL, _I, _P]),
@@ -269,6 +270,24 @@ def quantize_per_token(x):
           load().int8k_quantize_per_token(_ptr(x), _dtype_code(x), _ptr(q), _ptr(s), rows, cols,
                                           _stream(x)))
     return q, s
+
+
+def dequantize_per_token(q, scales, residual=None, dtype=None):
+    """y = (q.float() * scales[..., None]).to(dtype) [+ residual, in its dtype]."""
+    import torch
+
+    cols = q.shape[-1]
+    rows = q.numel() // cols
+    if residual is not None:
+        dtype = residual.dtype
+    elif dtype is None:
+        dtype = torch.float16
+    y = torch.empty(q.shape, dtype=dtype, device=q.device)
+    check("int8k_dequantize_per_token",
+          load().int8k_dequantize_per_token(_ptr(q), _ptr(scales), _dtype_code(y),
+                                            _ptr(residual) if residual is not None else None,
+                                            _ptr(y), rows, cols, _stream(q)))
+    return y
 
 
 def kv_cache_append(k_new, v_new, K_cache, V_cache, sK_cache, sV_cache, pos: int):

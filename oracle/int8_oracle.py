@@ -26,6 +26,10 @@ How each function is pinned (tests/test_oracle.py):
   mlp_forward : stage-by-stage against the pieces above on small shapes plus
       KATs (zero input -> zero output codes; constant input -> one code).
   quantize_fp16_per_tensor / dequantize_int8_to_fp16 : closed form + KATs.
+  dequantize_per_token_residual : PyTorch's own ops on the CPU (the reference block
+      runs exactly those) for fp16/bf16/fp32 with and without a residual, and
+      crafted (q, s) pairs whose fp32 product double-rounds to a different fp16
+      than the exact product (the two-step rounding is what is pinned).
   layernorm_quantize_per_token : torch.nn.functional.layer_norm (an independent
       library routine) on the same inputs, then quantize_per_token; closed
       form for a two-valued row (y = +-1 -> codes +-127).
@@ -338,6 +342,17 @@ def _round_to(y, dtype):
         u = y.view(np.uint32).astype(np.uint64)
         r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
         return r.view(np.float32)
+    return y
+
+
+def dequantize_per_token_residual(q, s, dtype="f16", residual=None):
+    """Consumer side of the block's INT8 MLP: (q.float() * s[..., None]).to(dtype), then
+    residual + that in the residual's dtype (bench/bench_block.py:107-113, 126-127).
+    Every step rounds on its own: the fp32 product, then `dtype`; with a residual the
+    fp32 sum of the two `dtype` values, then `dtype` again.  Returns float32 values."""
+    y = _round_to(np.asarray(q, F32) * np.asarray(s, F32)[..., None], dtype)
+    if residual is not None:
+        y = _round_to(np.asarray(residual, F32) + y, dtype)
     return y
 
 

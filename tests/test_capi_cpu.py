@@ -102,6 +102,12 @@ def test_mlp_argument_validation(capi):
 
 def test_quant_argument_validation(capi):
     lib = capi.load()
+    # per-token dequant: unknown dtype, misaligned scales
+    assert lib.int8k_dequantize_per_token(_fake(0x10000), _fake(0x20000), 5, None,
+                                          _fake(0x30000), 4, 64,
+                                          None) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert lib.int8k_dequantize_per_token(_fake(0x10000), _fake(0x20002), 0, None,
+                                          _fake(0x30000), 4, 64, None) == capi.INT8K_ERR_MISALIGNED
     assert lib.int8k_quantize_per_token(_fake(0x10000), 7, _fake(0x20000), _fake(0x30000), 4,
                                         64, None) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert lib.int8k_quantize_per_token(_fake(0x10001), 0, _fake(0x20000), _fake(0x30000), 4,

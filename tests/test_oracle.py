@@ -290,6 +290,38 @@ def test_quant_utils_per_tensor():
     np.testing.assert_array_equal(d, np.array([-64.0, 0.0, 63.5], np.float16))
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("residual", [False, True])
+def test_dequantize_per_token_residual_matches_torch(dtype, residual):
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    g = torch.Generator().manual_seed(7)
+    q = torch.randint(-128, 128, (33, 256), generator=g, dtype=torch.int8)
+    s = torch.rand(33, generator=g) * 0.05 + 1e-3
+    ref = (q.float() * s.unsqueeze(-1)).to(tdt)
+    r = None
+    if residual:
+        r = (torch.randn(33, 256, generator=g) * 4).to(tdt)
+        ref = r + ref
+    got = O.dequantize_per_token_residual(q.numpy(), s.numpy(), dtype,
+                                          None if r is None else r.float().numpy())
+    np.testing.assert_array_equal(got, ref.float().numpy())
+
+
+def test_dequantize_per_token_residual_double_rounding():
+    # (q, s) = (63, 0.04983569) etc.: pairs whose fp32 product sits on an fp16 tie that
+    # the exact product misses; the oracle must round through fp32 as torch does
+    rng = np.random.default_rng(11)
+    q = rng.integers(-128, 128, 1 << 16).astype(np.int8)
+    s = rng.uniform(1e-3, 0.05, 1 << 16).astype(np.float32)
+    once = (q.astype(np.float64) * s.astype(np.float64)).astype(np.float16)
+    hit = np.nonzero((q.astype(np.float32) * s).astype(np.float16) != once)[0]
+    assert hit.size > 0
+    got = O.dequantize_per_token_residual(q[hit, None], s[hit], "f16")[:, 0]
+    want = (torch.from_numpy(q[hit]).float() * torch.from_numpy(s[hit])).half()
+    np.testing.assert_array_equal(got, want.float().numpy())
+    assert not np.array_equal(got, once[hit].astype(np.float32))
+
+
 def _contiguous_as_pages(K, P):
     """[B, H, S, D] -> pages [B*npp, H, P, D] with sequence b in pages b*npp .. (b+1)*npp-1."""
     B, H, S = K.shape[:3]

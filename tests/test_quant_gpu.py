@@ -141,3 +141,96 @@ def test_quantize_per_token_beyond_2p32_work_items(ext, gpu):
     idx = torch.tensor([0, 1, rows // 2, rows - 5, rows - 1], device=gpu)
     rq, rs = workloads.quantize_per_token(x[idx].cpu())
     assert torch.equal(q[idx].cpu(), rq) and torch.equal(s[idx].cpu(), rs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(3, 64), (129, 1024), (2, 5, 48), (7, 33)])
+@pytest.mark.parametrize("residual", [False, True])
+def test_dequantize_per_token_matches_torch(ext, gpu, dtype, shape, residual):
+    # y = (q.float() * s[..., None]).to(dtype) (+ residual in its dtype), bit for bit;
+    # (7, 33) and (2, 5, 48) also take the one-element-per-thread kernel
+    g = torch.Generator().manual_seed(sum(shape) + residual)
+    q = torch.randint(-128, 128, shape, generator=g, dtype=torch.int8).to(gpu)
+    s = (torch.rand(shape[:-1], generator=g) * 0.05 + 1e-3).to(gpu)
+    ref = (q.float() * s.unsqueeze(-1)).to(dtype)
+    r = None
+    if residual:
+        r = (torch.randn(shape, generator=g) * 4).to(dtype).to(gpu)
+        ref = r + ref
+    y = ext.dequantize_per_token(q, s, residual=r, dtype=dtype)
+    torch.cuda.synchronize()
+    assert y.dtype == dtype and y.shape == q.shape
+    assert torch.equal(y, ref)
+    odt = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[dtype]
+    want = O.dequantize_per_token_residual(q.cpu().numpy(), s.cpu().numpy(), odt,
+                                           None if r is None else r.float().cpu().numpy())
+    np.testing.assert_array_equal(y.float().cpu().numpy(), want)
+
+
+def test_dequantize_per_token_capi_unaligned(gpu):
+    # an output that is not 16-byte aligned takes the one-element-per-thread kernel
+    rows, cols = 5, 64
+    q = torch.randint(-128, 128, (rows, cols), dtype=torch.int8,
+                      generator=torch.Generator().manual_seed(9)).to(gpu)
+    s = torch.rand(rows, generator=torch.Generator().manual_seed(10)).to(gpu)
+    base = torch.empty(rows * cols + 1, dtype=torch.float16, device=gpu)
+    y = capi.dequantize_per_token(q, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y, (q.float() * s[:, None]).half())
+    out = base[1:].view(rows, cols)
+    st = capi.load().int8k_dequantize_per_token(
+        capi._ptr(q), capi._ptr(s), capi.DTYPE_F16, None, capi._ptr(out), rows, cols,
+        capi._stream(q))
+    assert st == capi.INT8K_OK
+    torch.cuda.synchronize()
+    assert torch.equal(out, (q.float() * s[:, None]).half())
+
+
+def _fp16_double_rounding_cases(rng, count):
+    """(q, s) pairs with half(fp32(q * s)) != half(q * s): the fp32 product lands on
+    an fp16 tie that the exact product does not.  The dequantizers must give the
+    first (PyTorch's and the reference's rounding), not the fused single rounding."""
+    qs, ss = [], []
+    while len(qs) < count:
+        q = rng.integers(-128, 128, 1 << 16).astype(np.int8)
+        s = rng.uniform(1e-3, 0.05, 1 << 16).astype(np.float32)
+        twice = (q.astype(np.float32) * s).astype(np.float16)
+        once = (q.astype(np.float64) * s.astype(np.float64)).astype(np.float16)
+        hit = np.nonzero(twice != once)[0]
+        qs += list(q[hit]); ss += list(s[hit])
+    return np.array(qs[:count], np.int8), np.array(ss[:count], np.float32)
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_dequantize_fp16_rounds_through_fp32(ext, gpu, residual):
+    # regression: hipcc folds half(float(q) * s) into one fused rounding unless the
+    # fp32 product is pinned; 64 rows of 16 equal codes, one crafted (q, s) per row
+    rng = np.random.default_rng(11)
+    qv, sv = _fp16_double_rounding_cases(rng, 64)
+    q = torch.from_numpy(np.repeat(qv[:, None], 16, axis=1)).to(gpu)
+    s = torch.from_numpy(sv).to(gpu)
+    ref = (q.float() * s[:, None]).half()
+    r = None
+    if residual:
+        r = torch.zeros(64, 16, dtype=torch.float16, device=gpu)
+        ref = r + ref
+    y = ext.dequantize_per_token(q, s, residual=r, dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    assert not torch.equal(y.cpu(), torch.from_numpy(
+        (qv.astype(np.float64) * sv.astype(np.float64)).astype(np.float16))[:, None].expand(64, 16))
+
+
+def test_dequantize_int8_to_fp16_rounds_through_fp32(ext, gpu):
+    # the per-tensor dequantizer, same regression: one scale whose products with some
+    # of the 256 codes double-round differently from the fused rounding
+    rng = np.random.default_rng(12)
+    codes = np.arange(-128, 128, dtype=np.int8)
+    while True:
+        s = np.float32(rng.uniform(1e-3, 0.05))
+        twice = (codes.astype(np.float32) * s).astype(np.float16)
+        if (twice != (codes.astype(np.float64) * np.float64(s)).astype(np.float16)).any():
+            break
+    y = ext.dequantize_int8_to_fp16(torch.from_numpy(codes).to(gpu), float(s))
+    np.testing.assert_array_equal(y.cpu().numpy(), O.dequantize_int8_to_fp16(codes, s))
+    np.testing.assert_array_equal(y.cpu().numpy(), twice)
