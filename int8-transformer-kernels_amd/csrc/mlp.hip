@@ -50,10 +50,170 @@ struct EpiParams {
     float* pmax;         // [tiles_n][M] row absmax partials
 };
 
-// GELU, tanh form: 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi)(x + 0.044715 x^3).
+// GELU, tanh form: 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi)(x + 0.044715 x^3),
+// as x / (1 + 2^y) with y = -2 log2(e) u = x (c0 + c1 x^2): four VALU ops, exp and rcp.
+__device__ __forceinline__ float gelu_exponent(float x) {
+    constexpr float c0 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654);
+    constexpr float c1 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654 * 0.044715);
+    return x * __builtin_fmaf(c1, x * x, c0);
+}
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    return x * __builtin_amdgcn_rcpf(1.f + fast_exp2(-2.f * kLog2e * u));
+    return x * __builtin_amdgcn_rcpf(1.f + fast_exp2(gelu_exponent(x)));
+}
+
+// Row scales, column scales and bias of a tile, parked in LDS after the main
+// loop's stages: 3 x 256 floats.
+constexpr int kEpiLdsBytes = LDS_BYTES + 3 * BM * 4;
+static_assert(BM == kThreads && BN == kThreads, "one scale of each kind per thread");
+
+// Epilogue value of accumulator element acc with row scale sa, column scale sb, bias b.
+template <int EPI>
+__device__ __forceinline__ float epi_value(int acc, float sa, float sb, float b) {
+    float v = static_cast<float>(acc) * sa * sb;
+    if constexpr (EPI == EPI_GELU_F16) v = gelu_tanh(v + b);
+    return v;
+}
+
+// Row maxima of one 32-row block of a wave's sub-tile: rmax[r] holds the lane's
+// max over its columns for row acc_row(r, lane).  The max over the 32 lanes
+// that share those rows (one half of the wave) is taken stage by stage for
+// all 16 rows: DPP inside each 16-lane row, then v_permlane16_swap across the
+// two rows of the half (VALU only, no LDS round trip).  Lanes 0 and 32 then
+// write the 16 values as four runs of 4 consecutive rows into `slot` (the
+// block's rows of this wave's column half).
+__device__ __forceinline__ void tile_rowmax(const float (&rmax)[16], int* slot, int lane) {
+    int m[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = __float_as_int(rmax[r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = max(m[r], dpp_xor1(m[r]));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = max(m[r], dpp_xor2(m[r]));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = max(m[r], dpp_half_mirror(m[r]));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = max(m[r], dpp_row_mirror(m[r]));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const auto s = __builtin_amdgcn_permlane16_swap(m[r], m[r], false, false);
+        m[r] = max((int)s[0], (int)s[1]);
+    }
+    if ((lane & 31) == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<int4*>(slot + q * 8 + (lane >> 5) * 4) =
+                make_int4(m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]);
+    }
+}
+
+// Interior tiles (every row and column in range, BM * ldc * 2 < 2^32): the
+// fp16 tile goes out through a buffer resource at the tile's corner, so each
+// store's address is the lane's fixed offset plus a uniform (scalar) one.
+// Rows r, r+1 of a column sit in one lane and columns c, c+1 in lanes 2k,
+// 2k+1: the lane converts its pair of rows into one word (v_cvt_pk_f16_f32),
+// swaps it with the neighbour lane (DPP), and one byte permute leaves the
+// even lane (r, c..c+1) and the odd lane (r+1, c..c+1) to store as one dword.
+template <int EPI>
+__device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM][TN], const EpiParams& p,
+                                                  int m0, int n0, int* rowmax, const float* esa,
+                                                  const float* esb, const float* ebias) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const bool odd = lane & 1;
+    const __amdgpu_buffer_rsrc_t out =
+        make_buffer(p.c16 + (size_t)m0 * p.ldc + n0, (uint32_t)(BM * p.ldc * 2));
+    const uint32_t voff =
+        ((uint32_t)(wm * WM + (lane >> 5) * 4 + (odd ? 1 : 0)) * p.ldc + wn * WN + (lane & 30)) * 2;
+    const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+    float sbv[TN], biv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        sbv[j] = esb[wn * WN + j * 32 + (lane & 31)];
+        biv[j] = ebias[wn * WN + j * 32 + (lane & 31)];
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        // rows (r/4)*8 + (lane/32)*4 + r%4: four runs of 4 consecutive rows
+        float sav[16], rmax[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 s4 =
+                *reinterpret_cast<const float4*>(esa + wm * WM + i * 32 + q * 8 + (lane >> 5) * 4);
+            sav[4 * q] = s4.x, sav[4 * q + 1] = s4.y, sav[4 * q + 2] = s4.z, sav[4 * q + 3] = s4.w;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            // stage by stage over the 16 elements, so one wave per SIMD has
+            // independent work between the dependent steps of each element
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = static_cast<float>(acc[i][j][r]) * sav[r] * sbv[j];
+            if constexpr (EPI == EPI_GELU_F16) {
+                float e[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = v[r] + biv[j];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) e[r] = gelu_exponent(v[r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) e[r] = fast_exp2(e[r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_rcpf(1.f + e[r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = v[r] * e[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) rmax[r] = fmaxf(rmax[r], fabsf(v[r]));
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const h2 h = __builtin_convertvector((f2){v[r], v[r + 1]}, h2);
+                const uint32_t own = __builtin_bit_cast(uint32_t, h);
+                const uint32_t nb = __builtin_amdgcn_mov_dpp(own, 0xB1, 0xF, 0xF, true);
+                const uint32_t word = __builtin_amdgcn_perm(nb, own, sel);
+                const uint32_t soff = ((uint32_t)(i * 32 + (r >> 2) * 8 + (r & 3)) * p.ldc + j * 32) * 2;
+                __builtin_amdgcn_raw_buffer_store_b32(word, out, voff, soff, 0);
+            }
+        }
+        tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
+    }
+}
+
+// Tiles on the matrix edge: the same values, element stores guarded by row < M
+// and column < N, and the row maxima over in-range columns only.
+template <int EPI>
+__device__ __forceinline__ void epilogue_edge(const v16i (&acc)[TM][TN], const EpiParams& p,
+                                              int M, int N, int m0, int n0, int* rowmax,
+                                              const float* esa, const float* esb,
+                                              const float* ebias) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int rbase = m0 + wm * WM;
+    const int cbase = n0 + wn * WN + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        float rmax[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int cl = wn * WN + j * 32 + (lane & 31);
+            const bool cok = n0 + cl < N;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = wm * WM + i * 32 + acc_row(r, lane);
+                const float v = epi_value<EPI>(acc[i][j][r], esa[rl], esb[cl], ebias[cl]);
+                if (cok) rmax[r] = fmaxf(rmax[r], fabsf(v));
+                const int row = rbase + i * 32 + acc_row(r, lane);
+                if (row < M && cok) p.c16[(size_t)row * p.ldc + cbase + j * 32] = f32_to_f16_bits(v);
+            }
+        }
+        tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
+    }
 }
 
 template <int EPI>
@@ -64,6 +224,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    // The epilogue's scales and bias for this tile, loaded before the main loop
+    // (clamped indices, so unconditional) so the loop hides their latency.
+    float pre_sa = 0.f, pre_sb = 0.f, pre_b = 0.f;
+    if constexpr (EPI != EPI_I32) {
+        const int t = threadIdx.x;
+        pre_sa = p.sa[(size_t)min(m0 + t, M - 1) * p.sa_stride];
+        pre_sb = p.sb[(size_t)min(n0 + t, N - 1) * p.sb_stride];
+        if (p.bias != nullptr) pre_b = p.bias[min(n0 + t, N - 1)];
+    }
     v16i acc[TM][TN];
     // interior tiles take the unmasked operand path
     if (m0 + BM <= M && n0 + BN <= N && K % BK == 0)
@@ -71,13 +240,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     else
         mainloop<true>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int rbase = m0 + wm * WM;
-    const int cbase = n0 + wn * WN + (lane & 31);
-
     if constexpr (EPI == EPI_I32) {
+        const int lane = threadIdx.x & 63;
+        const int wave = threadIdx.x >> 6;
+        const int wm = wave >> 1, wn = wave & 1;
+        const int rbase = m0 + wm * WM;
+        const int cbase = n0 + wn * WN + (lane & 31);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -91,81 +259,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
             }
         return;
     } else {
-        // Row absmax of this block's tile, gathered in LDS (values >= 0, so
-        // integer max on the bit pattern orders them like floats).
+        // Row absmax of this block's tile: rowmax[wn][row] from each column
+        // half of the waves, combined below (values >= 0, so integer max on
+        // the bit pattern orders them like floats).  The scale region lies
+        // past the stages; the row maxima reuse stage 0, whose last reads
+        // (operands past the end of K) are never used.
         int* rowmax = reinterpret_cast<int*>(lds);
-        for (int i = threadIdx.x; i < BM; i += kThreads) rowmax[i] = 0;
+        float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
+        float* esb = esa + BM;
+        float* ebias = esb + BN;
+        esa[threadIdx.x] = pre_sa;
+        esb[threadIdx.x] = pre_sb;
+        ebias[threadIdx.x] = pre_b;
         __syncthreads();
-        const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
-        const bool odd = lane & 1;
-        float sbv[TN], biv[TN];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = cbase + j * 32;
-            sbv[j] = col < N ? p.sb[(size_t)col * p.sb_stride] : 0.f;
-            biv[j] = (p.bias != nullptr && col < N) ? p.bias[col] : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            float sav[16], rmax[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = rbase + i * 32 + acc_row(r, lane);
-                sav[r] = row < M ? p.sa[(size_t)row * p.sa_stride] : 0.f;
-                rmax[r] = 0.f;
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = cbase + j * 32;
-                const bool cok = col < N;
-                float v[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    v[r] = static_cast<float>(acc[i][j][r]) * sav[r] * sbv[j];
-                    if constexpr (EPI == EPI_GELU_F16) v[r] = gelu_tanh(v[r] + biv[j]);
-                    if (cok) rmax[r] = fmaxf(rmax[r], fabsf(v[r]));
-                }
-                if (interior) {
-                    // Rows r, r+1 are consecutive; lanes 2k, 2k+1 hold columns c, c+1.
-                    // Exchange one half so the even lane stores (r, c..c+1) and the
-                    // odd lane (r+1, c..c+1) as one 32-bit word each.
-#pragma unroll
-                    for (int r = 0; r < 16; r += 2) {
-                        const uint32_t h0 = f32_to_f16_bits(v[r]);
-                        const uint32_t h1 = f32_to_f16_bits(v[r + 1]);
-                        const uint32_t recv = (uint32_t)dpp_xor1((int)(odd ? h0 : h1));
-                        const uint32_t word = odd ? (recv | (h1 << 16)) : (h0 | (recv << 16));
-                        const int row = rbase + i * 32 + acc_row(r, lane) + (odd ? 1 : 0);
-                        *reinterpret_cast<uint32_t*>(p.c16 + (size_t)row * p.ldc + (col & ~1)) =
-                            word;
-                    }
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int row = rbase + i * 32 + acc_row(r, lane);
-                        if (row < M && cok)
-                            p.c16[(size_t)row * p.ldc + col] = f32_to_f16_bits(v[r]);
-                    }
-                }
-            }
-            // Max over the 32 lanes that share these rows: DPP inside each
-            // 16-lane row, then one swizzle across the two rows of the half.
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                int m = __float_as_int(rmax[r]);
-                m = max(m, dpp_xor1(m));
-                m = max(m, dpp_xor2(m));
-                m = max(m, dpp_half_mirror(m));
-                m = max(m, dpp_row_mirror(m));
-                m = max(m, __builtin_amdgcn_ds_swizzle(m, 0x401f));
-                if ((lane & 31) == 0) atomicMax(&rowmax[wm * WM + i * 32 + acc_row(r, lane)], m);
-            }
-        }
+        if (m0 + BM <= M && n0 + BN <= N && (size_t)BM * p.ldc * 2 < (1ull << 32))
+            epilogue_interior<EPI>(acc, p, m0, n0, rowmax, esa, esb, ebias);
+        else
+            epilogue_edge<EPI>(acc, p, M, N, m0, n0, rowmax, esa, esb, ebias);
         __syncthreads();
-        for (int i = threadIdx.x; i < BM; i += kThreads) {
-            const int row = m0 + i;
-            if (row < M) p.pmax[(size_t)tn * M + row] = __int_as_float(rowmax[i]);
-        }
+        const int row = m0 + threadIdx.x;
+        if (row < M)
+            p.pmax[(size_t)tn * M + row] =
+                __int_as_float(max(rowmax[threadIdx.x], rowmax[BM + threadIdx.x]));
     }
 }
 
@@ -415,7 +530,8 @@ template <int EPI>
 int launch_gemm(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
                 hipStream_t stream) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    gemm_i8_kernel<EPI><<<tiles_m * tiles_n, kThreads, LDS_BYTES, stream>>>(
+    gemm_i8_kernel<EPI><<<tiles_m * tiles_n, kThreads, EPI == EPI_I32 ? LDS_BYTES : kEpiLdsBytes,
+                          stream>>>(
         A, Bt, M, N, K, K, K, tiles_m, tiles_n, p);
     return check_launch("gemm_i8_kernel");
 }
@@ -474,10 +590,10 @@ int configure_lds() {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
     if (e == hipSuccess)
         e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_GELU_F16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
     if (e == hipSuccess)
         e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
     if (e != hipSuccess) {
         set_last_error("hipFuncSetAttribute", e);
         return INT8K_ERR_HIP;
