@@ -146,6 +146,7 @@ __device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM][TN], con
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
+        uint32_t words[TN][8];  // packed fp16 pairs, stored once all TN are done
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             // stage by stage over the 16 elements, so one wave per SIMD has
@@ -173,11 +174,18 @@ __device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM][TN], con
                 const h2 h = __builtin_convertvector((f2){v[r], v[r + 1]}, h2);
                 const uint32_t own = __builtin_bit_cast(uint32_t, h);
                 const uint32_t nb = __builtin_amdgcn_mov_dpp(own, 0xB1, 0xF, 0xF, true);
-                const uint32_t word = __builtin_amdgcn_perm(nb, own, sel);
-                const uint32_t soff = ((uint32_t)(i * 32 + (r >> 2) * 8 + (r & 3)) * p.ldc + j * 32) * 2;
-                __builtin_amdgcn_raw_buffer_store_b32(word, out, voff, soff, 0);
+                words[j][r >> 1] = __builtin_amdgcn_perm(nb, own, sel);
             }
         }
+        // row by row, the TN stores of a row back to back: the 64-byte pieces
+        // of each 128-byte line reach the cache together
+#pragma unroll
+        for (int r = 0; r < 16; r += 2)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t soff = ((uint32_t)(i * 32 + (r >> 2) * 8 + (r & 3)) * p.ldc + j * 32) * 2;
+                __builtin_amdgcn_raw_buffer_store_b32(words[j][r >> 1], out, voff, soff, 0);
+            }
         tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
     }
 }
