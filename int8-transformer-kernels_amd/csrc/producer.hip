@@ -275,9 +275,13 @@ __global__ __launch_bounds__(256) void layernorm_quant_vec_kernel(
     }
 }
 
-// Split-heads + per-token quantizer: source row r = ((b S + s) parts + p) H + h
-// of Dh elements, 1 << lg lanes per row, one 16-byte chunk per lane.  Each wave
-// takes U row groups of its grid stride at a time (U loads per lane in flight).
+// Split-heads + per-token quantizer: source row ((b S + s) parts + p) H + h of
+// Dh elements, 1 << lg lanes per row, one 16-byte chunk per lane.  Rows are
+// walked in destination order k = ((p B + b) H + h) S + s, so the rows of a
+// wave are consecutive tokens of one head: its codes and scales go out as one
+// contiguous run (not as 64-byte pieces of H different heads), while each row
+// is still read as one full source row.  Each wave takes U row groups of its
+// grid stride at a time (U loads per lane in flight).
 template <int DT, int U>
 __global__ __launch_bounds__(256) void quant_heads_vec_kernel(
     const void* __restrict__ x, int8_t* __restrict__ q0, float* __restrict__ s0,
@@ -290,35 +294,37 @@ __global__ __launch_bounds__(256) void quant_heads_vec_kernel(
     const int Dh = (1 << lg) * W;
     const uint4* src = reinterpret_cast<const uint4*>(x);
     const uint32_t stride = gridDim.x * 4 * rpw;
-    for (uint32_t rb = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; rb < rows; rb += U * stride) {
+    const uint32_t part_rows = rows / parts;  // B H S rows per part
+    for (uint32_t kb = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; kb < rows; kb += U * stride) {
         uint4 w[U];
+        uint32_t drow[U], pp[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             // rows past the end load the last row (no divergent branch around the
             // loads, so they all stay in flight) and are not stored
-            const uint32_t r = min(rb + u * stride + (lane >> lg), rows - 1);
+            const uint32_t k = min(kb + u * stride + (lane >> lg), rows - 1);
+            pp[u] = k / part_rows;
+            drow[u] = k - pp[u] * part_rows;  // (b H + h) S + s
+            const uint32_t bh = drow[u] / S, s = drow[u] - bh * S;
+            const uint32_t b = bh / H, h = bh - b * H;
+            const uint32_t r = ((b * S + s) * parts + pp[u]) * H + h;
             w[u] = src[((size_t)r << lg) + c0];
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t r = rb + u * stride + (lane >> lg);
             float v[W];
             unpack_chunk<DT>(w[u], v);
             float m = 0.f;
 #pragma unroll
             for (int e = 0; e < W; ++e) m = fmaxf(m, fabsf(v[e]));
             m = row_reduce(m, lg, [](float a, float b) { return fmaxf(a, b); });
-            if (r >= rows) continue;
+            if (kb + u * stride + (lane >> lg) >= rows) continue;
             const float sc = fmaxf(m, 1e-8f) / 127.f;
             const float inv = 1.f / sc;
-            const uint32_t h = r % H, r1 = r / H;
-            const uint32_t p = r1 % parts, tok = r1 / parts;
-            const uint32_t b = tok / S, s = tok - b * S;
-            const size_t drow = ((size_t)b * H + h) * S + s;  // [B, H, S] row of the part
-            int8_t* q = p == 0 ? q0 : (p == 1 ? q1 : q2);
-            float* sp = p == 0 ? s0 : (p == 1 ? s1 : s2);
-            store_codes<W>(v, sc, inv, q + drow * Dh + (size_t)c0 * W);
-            if (c0 == 0) sp[drow] = sc;
+            int8_t* q = pp[u] == 0 ? q0 : (pp[u] == 1 ? q1 : q2);
+            float* sp = pp[u] == 0 ? s0 : (pp[u] == 1 ? s1 : s2);
+            store_codes<W>(v, sc, inv, q + (size_t)drow[u] * Dh + (size_t)c0 * W);
+            if (c0 == 0) sp[drow[u]] = sc;
         }
     }
 }
