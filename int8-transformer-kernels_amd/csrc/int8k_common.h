@@ -110,9 +110,11 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
 // half(a * b) into v_fma_mixlo_f16, which rounds the exact product to fp16 in
 // one step; PyTorch's (q.float() * s).half() rounds it to fp32 first, and the
 // two differ when that first rounding lands on an fp16 tie.  The empty asm
-// pins x as the fp32 value, for outputs that must match bit for bit.
+// pins x as the fp32 value, for outputs that must match bit for bit (not
+// volatile: a volatile asm would also keep loads from being merged or moved
+// across it).
 __device__ __forceinline__ __half f16_of_f32(float x) {
-    asm volatile("" : "+v"(x));
+    asm("" : "+v"(x));
     return __float2half_rn(x);
 }
 

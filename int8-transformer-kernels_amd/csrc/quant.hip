@@ -244,6 +244,16 @@ __global__ __launch_bounds__(256) void dequant_rows_vec_kernel(const int8_t* __r
                                                                uint32_t chunks, uint32_t cpr) {
 #pragma clang fp contract(off)
     for (uint32_t g = blockIdx.x * 256 + threadIdx.x; g < chunks; g += gridDim.x * 256) {
+        // 16 residual values: 2 (fp16/bf16) or 4 (fp32) 16-byte words
+        constexpr int RW = DT == INT8K_DTYPE_F32 ? 4 : 2;
+        uint32_t rd[4 * RW];
+        if constexpr (RES) {
+#pragma unroll
+            for (int j = 0; j < RW; ++j) {
+                const uint4 r = reinterpret_cast<const uint4*>(res)[(size_t)g * RW + j];
+                rd[4 * j] = r.x, rd[4 * j + 1] = r.y, rd[4 * j + 2] = r.z, rd[4 * j + 3] = r.w;
+            }
+        }
         const uint4 w = reinterpret_cast<const uint4*>(q)[g];
         const float s = sc[g / cpr];
         const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
@@ -253,8 +263,14 @@ __global__ __launch_bounds__(256) void dequant_rows_vec_kernel(const int8_t* __r
             v[i] = round_dtype<DT>((float)(int8_t)(wd[i >> 2] >> (8 * (i & 3))) * s);
         if constexpr (RES) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                v[i] = round_dtype<DT>(load_dtype<DT>(res, (size_t)g * 16 + i) + v[i]);
+            for (int i = 0; i < 16; ++i) {
+                float r;
+                if constexpr (DT == INT8K_DTYPE_F32) r = __uint_as_float(rd[i]);
+                else if constexpr (DT == INT8K_DTYPE_F16)
+                    r = __half2float(__ushort_as_half((unsigned short)(rd[i >> 1] >> (16 * (i & 1)))));
+                else r = __uint_as_float((rd[i >> 1] >> (16 * (i & 1))) << 16);
+                v[i] = round_dtype<DT>(r + v[i]);
+            }
         }
         if constexpr (DT == INT8K_DTYPE_F32) {
             float4* o = reinterpret_cast<float4*>(y) + (size_t)g * 4;
