@@ -74,6 +74,15 @@ int int8k_decode_attention_forward(
     int BH, int S, int head_dim, int nsplit,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same decode emitting int8 rows: out_q int8 [BH, D] and out_scale fp32
+ * [BH], the per-token quantization of the fp16 rows the call above returns
+ * (as int8k_attention_forward_quant for prefill).  Same workspace. */
+int int8k_decode_attention_forward_quant(
+    const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* out_q, float* out_scale,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int BH, int S, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream);
+
 /* The split count the forward call uses for this shape (after clamping). */
 int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
 
@@ -86,6 +95,14 @@ int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
 int int8k_decode_attention_forward_cache(
     const int8_t* Q, const int8_t* K_cache, const int8_t* V_cache, uint16_t* out,
     const float* scale_Q, const float* sK_cache, const float* sV_cache,
+    int BH, int S, int capacity, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* int8 rows (out_q [BH, D], out_scale [BH]) from the cache decode; see
+ * int8k_decode_attention_forward_quant. */
+int int8k_decode_attention_forward_cache_quant(
+    const int8_t* Q, const int8_t* K_cache, const int8_t* V_cache, int8_t* out_q,
+    float* out_scale, const float* scale_Q, const float* sK_cache, const float* sV_cache,
     int BH, int S, int capacity, int head_dim, int nsplit,
     void* workspace, size_t workspace_bytes, void* stream);
 
@@ -119,6 +136,15 @@ int int8k_decode_attention_forward_paged(
     int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
     int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream);
 
+/* int8 rows (out_q [B, H, D], out_scale [B*H]) from the paged decode; see
+ * int8k_decode_attention_forward_quant. */
+int int8k_decode_attention_forward_paged_quant(
+    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, int8_t* out_q,
+    float* out_scale, const float* scale_Q, const float* sK_pages, const float* sV_pages,
+    const int32_t* block_tables, const int32_t* context_lens,
+    int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
+    int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* INT8 prefill attention (seq_q == seq_kv).                                 */
 /*                                                                          */
@@ -137,6 +163,19 @@ int int8k_decode_attention_forward_paged(
 /* ------------------------------------------------------------------------ */
 int int8k_attention_forward(
     const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int batch, int heads, int seq_len, int head_dim, int causal, void* stream);
+
+/* Attention output emitted as the next INT8 stage's input: out_q int8
+ * [batch, heads, seq_len, head_dim] and out_scale fp32 [batch*heads*seq_len],
+ * the per-token quantization (int8k_quantize_per_token) of the fp16 rows
+ * int8k_attention_forward returns, byte for byte, without their round trip
+ * through memory.  The attention-output producer fusion the reference names
+ * as its next lever (OPTIMIZATION.md:241-246; its callers quantize in
+ * PyTorch, bench/bench_block.py:59-63); no counterpart in its kernels.
+ * out_q and out_scale 4-byte aligned; otherwise as int8k_attention_forward. */
+int int8k_attention_forward_quant(
+    const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* out_q, float* out_scale,
     const float* scale_Q, const float* scale_K, const float* scale_V,
     int batch, int heads, int seq_len, int head_dim, int causal, void* stream);
 

@@ -34,6 +34,7 @@
 #include <cstdlib>
 
 #include "int8k_common.h"
+#include "rows.h"
 
 namespace int8k {
 namespace {
@@ -288,7 +289,7 @@ __device__ __forceinline__ void finish_unit(float m, float l, float* acc, int gr
             const float inv = L > 0.f ? 1.f / L : 0.f;
             uint16_t h[16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) h[e] = f32_to_f16_bits(acc[e] * inv);
+            for (int e = 0; e < 16; ++e) h[e] = __half_as_ushort(f16_of_f32(acc[e] * inv));
             uint4* dst = reinterpret_cast<uint4*>(out + (size_t)unit * D + sub * 16);
             dst[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                                 h[6] | (h[7] << 16));
@@ -363,11 +364,14 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
     finish_unit<D, FINAL>(m, l, acc, grp, sub, unit, part_ml, part_acc, out);
 }
 
-// Pass 2: one wave per bh merges its nsplit partial states into fp16.
+// Pass 2: one wave per bh merges its nsplit partial states into the fp16 row,
+// or with qout set into the per-token int8 quantization of that fp16 row
+// (codes and scale as int8k_quantize_per_token gives for it).
 template <int D>
 __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
     const float* __restrict__ part_ml, const float* __restrict__ part_acc,
-    uint16_t* __restrict__ out, int BH, int nsplit) {
+    uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qscale, int BH,
+    int nsplit) {
     constexpr int DPL = D / 64;  // dims per lane
     const int lane = threadIdx.x & 63;
     const int bh = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
@@ -395,9 +399,25 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
         for (int i = 0; i < DPL; ++i) acc[i] = fmaf(pa[(size_t)s * D + i], w, acc[i]);
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;  // no rows at all (empty sequence): zeros
+    float y[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) y[i] = __half2float(f16_of_f32(acc[i] * inv));
+    if (qout != nullptr) {
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) am = fmaxf(am, fabsf(y[i]));
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+        const float sc = fmaxf(am, 1e-8f) / 127.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i)
+            qout[(size_t)bh * D + lane * DPL + i] = (int8_t)quant_code(y[i], sc);
+        if (lane == 0) qscale[bh] = sc;
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < DPL; ++i)
-        out[(size_t)bh * D + lane * DPL + i] = f32_to_f16_bits(acc[i] * inv);
+        out[(size_t)bh * D + lane * DPL + i] = __half_as_ushort(__float2half_rn(y[i]));
 }
 
 // Paged variant of pass 1.  Unit = (b, h, split) as above, over positions
@@ -524,10 +544,18 @@ void launch_split_ns(int ns, int flags, int stagger, dim3 grid, hipStream_t stre
                                        S, S_cap, plan, units, qk);
 }
 
+// Where a decode writes its rows: fp16 `f16`, or int8 `q` + per-row scale `qs`.
+struct DecodeOut {
+    uint16_t* f16;
+    int8_t* q;
+    float* qs;
+};
+
 template <int D>
-int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, const DecodeOut& o,
                   const float* sQ, const float* sK, const float* sV, int BH, int S, int S_cap,
                   const SplitPlan& plan, const DecodeWorkspace& w, hipStream_t stream) {
+    uint16_t* out = o.f16;
     const long long units = (long long)BH * plan.nsplit;
     const float qk_scale_log2 = (1.0f / std::sqrt((float)D)) * kLog2e;
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
@@ -538,7 +566,8 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     const int sg = tn.stagger;
     const int u = (int)units;
     const float qk = qk_scale_log2;
-    const bool final_pass = plan.nsplit == 1 && aligned_to(out, 16);
+    // the in-kernel final write is fp16 only; int8 rows always go through the combine
+    const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
     if (vec && final_pass)
         launch_split_ns<D, true, true>(ns, fl, sg, grid, stream, Q, K, V, sQ, sK, sV, w, out, S, S_cap, plan, u, qk);
     else if (vec)
@@ -550,23 +579,24 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     int st = check_launch("decode_split_kernel");
     if (st != INT8K_OK || final_pass) return st;
     const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));
-    decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out, BH,
-                                                                  plan.nsplit);
+    decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out,
+                                                                  o.q, o.qs, BH, plan.nsplit);
     return check_launch("decode_combine_kernel");
 }
 
 template <int D>
-int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, uint16_t* out,
+int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, const DecodeOut& o,
                         const float* sQ, const float* sKp, const float* sVp,
                         const int32_t* tables, const int32_t* lens, int B, int H,
                         int num_pages, int log2_page, int max_pages, const SplitPlan& plan,
                         const DecodeWorkspace& w, hipStream_t stream) {
+    uint16_t* out = o.f16;
     const int BH = B * H;
     const long long units = (long long)BH * plan.nsplit;
     const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
     constexpr int NS = D == 128 ? 8 : 4;
-    const bool final_pass = plan.nsplit == 1 && aligned_to(out, 16);
+    const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
     if (final_pass)
         decode_paged_kernel<D, NS, true><<<grid, kBlockThreads, 0, stream>>>(
             Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,
@@ -578,8 +608,8 @@ int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, uin
     int st = check_launch("decode_paged_kernel");
     if (st != INT8K_OK || final_pass) return st;
     const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));
-    decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out, BH,
-                                                                  plan.nsplit);
+    decode_combine_kernel<D><<<gridc, kBlockThreads, 0, stream>>>(w.part_ml, w.part_acc, out,
+                                                                  o.q, o.qs, BH, plan.nsplit);
     return check_launch("decode_combine_kernel");
 }
 
@@ -599,17 +629,23 @@ extern "C" size_t int8k_decode_attention_workspace_bytes(int BH, int S, int head
     return carve(nullptr, (long long)BH * plan.nsplit, head_dim).bytes;
 }
 
-static int decode_impl(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+static bool out_ok(const DecodeOut& o) {
+    return o.f16 ? aligned_to(o.f16, 2) : (o.q != nullptr && o.qs != nullptr && aligned_to(o.qs, 4));
+}
+
+static int decode_impl(const int8_t* Q, const int8_t* K, const int8_t* V, const DecodeOut& out,
                        const float* scale_Q, const float* scale_K, const float* scale_V, int BH,
                        int S, int S_cap, int head_dim, int nsplit, void* workspace,
                        size_t workspace_bytes, void* stream) {
     clear_last_error();
-    if (!Q || !K || !V || !out || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
+    if (!Q || !K || !V || !(out.f16 || out.q) || !scale_Q || !scale_K || !scale_V)
+        return INT8K_ERR_INVALID_ARGUMENT;
     if (BH <= 0 || S <= 0 || S_cap < S || nsplit < 0) return INT8K_ERR_INVALID_ARGUMENT;
     if (head_dim != 64 && head_dim != 128) return INT8K_ERR_UNSUPPORTED;
+    if (!out.f16 && !out.qs) return INT8K_ERR_INVALID_ARGUMENT;
     if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) ||
         !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4) ||
-        !aligned_to(out, 2))
+        !out_ok(out))
         return INT8K_ERR_MISALIGNED;
     const SplitPlan plan = plan_splits(BH, S, head_dim, nsplit);
     const long long units = (long long)BH * plan.nsplit;
@@ -629,8 +665,19 @@ extern "C" int int8k_decode_attention_forward(
     const float* scale_Q, const float* scale_K, const float* scale_V,
     int BH, int S, int head_dim, int nsplit,
     void* workspace, size_t workspace_bytes, void* stream) {
-    return decode_impl(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, S, head_dim, nsplit,
-                       workspace, workspace_bytes, stream);
+    if (!out) return INT8K_ERR_INVALID_ARGUMENT;
+    return decode_impl(Q, K, V, DecodeOut{out, nullptr, nullptr}, scale_Q, scale_K, scale_V, BH,
+                       S, S, head_dim, nsplit, workspace, workspace_bytes, stream);
+}
+
+extern "C" int int8k_decode_attention_forward_quant(
+    const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* out_q, float* out_scale,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int BH, int S, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    if (!out_q || !out_scale) return INT8K_ERR_INVALID_ARGUMENT;
+    return decode_impl(Q, K, V, DecodeOut{nullptr, out_q, out_scale}, scale_Q, scale_K, scale_V,
+                       BH, S, S, head_dim, nsplit, workspace, workspace_bytes, stream);
 }
 
 extern "C" int int8k_decode_attention_forward_cache(
@@ -638,8 +685,21 @@ extern "C" int int8k_decode_attention_forward_cache(
     const float* scale_Q, const float* sK_cache, const float* sV_cache,
     int BH, int S, int capacity, int head_dim, int nsplit,
     void* workspace, size_t workspace_bytes, void* stream) {
-    return decode_impl(Q, K_cache, V_cache, out, scale_Q, sK_cache, sV_cache, BH, S, capacity,
-                       head_dim, nsplit, workspace, workspace_bytes, stream);
+    if (!out) return INT8K_ERR_INVALID_ARGUMENT;
+    return decode_impl(Q, K_cache, V_cache, DecodeOut{out, nullptr, nullptr}, scale_Q, sK_cache,
+                       sV_cache, BH, S, capacity, head_dim, nsplit, workspace, workspace_bytes,
+                       stream);
+}
+
+extern "C" int int8k_decode_attention_forward_cache_quant(
+    const int8_t* Q, const int8_t* K_cache, const int8_t* V_cache, int8_t* out_q,
+    float* out_scale, const float* scale_Q, const float* sK_cache, const float* sV_cache,
+    int BH, int S, int capacity, int head_dim, int nsplit,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    if (!out_q || !out_scale) return INT8K_ERR_INVALID_ARGUMENT;
+    return decode_impl(Q, K_cache, V_cache, DecodeOut{nullptr, out_q, out_scale}, scale_Q,
+                       sK_cache, sV_cache, BH, S, capacity, head_dim, nsplit, workspace,
+                       workspace_bytes, stream);
 }
 
 // The paged kernel always uses 8 slots for D = 128 and 4 for D = 64 (page_size
@@ -671,15 +731,15 @@ extern "C" size_t int8k_decode_attention_paged_workspace_bytes(int B, int H, int
     return carve(nullptr, BH * plan.nsplit, head_dim).bytes;
 }
 
-extern "C" int int8k_decode_attention_forward_paged(
-    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, uint16_t* out,
+static int paged_impl(
+    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, const DecodeOut& out,
     const float* scale_Q, const float* sK_pages, const float* sV_pages,
     const int32_t* block_tables, const int32_t* context_lens,
     int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
     int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream) {
     clear_last_error();
-    if (!Q || !K_pages || !V_pages || !out || !scale_Q || !sK_pages || !sV_pages ||
-        !block_tables || !context_lens)
+    if (!Q || !K_pages || !V_pages || !(out.f16 || (out.q && out.qs)) || !scale_Q || !sK_pages ||
+        !sV_pages || !block_tables || !context_lens)
         return INT8K_ERR_INVALID_ARGUMENT;
     if (B <= 0 || H <= 0 || num_pages <= 0 || max_pages_per_seq <= 0 || max_context <= 0 ||
         nsplit < 0)
@@ -693,7 +753,7 @@ extern "C" int int8k_decode_attention_forward_paged(
     if ((long long)num_pages * H * page_size * head_dim >= (1LL << 40)) return INT8K_ERR_UNSUPPORTED;
     if (!aligned_to(Q, 16) || !aligned_to(K_pages, 16) || !aligned_to(V_pages, 16) ||
         !aligned_to(scale_Q, 4) || !aligned_to(sK_pages, 4) || !aligned_to(sV_pages, 4) ||
-        !aligned_to(block_tables, 4) || !aligned_to(context_lens, 4) || !aligned_to(out, 2))
+        !aligned_to(block_tables, 4) || !aligned_to(context_lens, 4) || !out_ok(out))
         return INT8K_ERR_MISALIGNED;
     if (BH >= (1LL << 31)) return INT8K_ERR_UNSUPPORTED;
     const SplitPlan plan = plan_paged((int)BH, max_context, head_dim, nsplit);
@@ -711,4 +771,29 @@ extern "C" int int8k_decode_attention_forward_paged(
     return launch_decode_paged<64>(Q, K_pages, V_pages, out, scale_Q, sK_pages, sV_pages,
                                    block_tables, context_lens, B, H, num_pages, log2_page,
                                    max_pages_per_seq, plan, w, as_stream(stream));
+}
+
+extern "C" int int8k_decode_attention_forward_paged(
+    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, uint16_t* out,
+    const float* scale_Q, const float* sK_pages, const float* sV_pages,
+    const int32_t* block_tables, const int32_t* context_lens,
+    int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
+    int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!out) return INT8K_ERR_INVALID_ARGUMENT;
+    return paged_impl(Q, K_pages, V_pages, DecodeOut{out, nullptr, nullptr}, scale_Q, sK_pages,
+                      sV_pages, block_tables, context_lens, B, H, head_dim, num_pages, page_size,
+                      max_pages_per_seq, max_context, nsplit, workspace, workspace_bytes, stream);
+}
+
+extern "C" int int8k_decode_attention_forward_paged_quant(
+    const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, int8_t* out_q,
+    float* out_scale, const float* scale_Q, const float* sK_pages, const float* sV_pages,
+    const int32_t* block_tables, const int32_t* context_lens,
+    int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
+    int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!out_q || !out_scale) return INT8K_ERR_INVALID_ARGUMENT;
+    return paged_impl(Q, K_pages, V_pages, DecodeOut{nullptr, out_q, out_scale}, scale_Q,
+                      sK_pages, sV_pages, block_tables, context_lens, B, H, head_dim, num_pages,
+                      page_size, max_pages_per_seq, max_context, nsplit, workspace,
+                      workspace_bytes, stream);
 }

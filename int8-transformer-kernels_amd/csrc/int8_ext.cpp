@@ -57,9 +57,12 @@ torch::Tensor aligned_i8(const torch::Tensor& t) {
 // (batch, heads, seq_len, head_dim), all the same shape; per-token fp32 scales
 // with batch*heads*seq_len elements; returns fp16 of Q's shape.  `is_causal`
 // is a new optional trailing argument (default false = the reference's math).
-torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
-                                           torch::Tensor scale_Q, torch::Tensor scale_K,
-                                           torch::Tensor scale_V, bool is_causal) {
+// With `quant` the output is the per-token int8 of those fp16 rows: {int8 of
+// Q's shape, fp32 scales (batch, heads, seq_len)}.
+static std::vector<torch::Tensor> attention_impl(torch::Tensor Q, torch::Tensor K,
+                                                 torch::Tensor V, torch::Tensor scale_Q,
+                                                 torch::Tensor scale_K, torch::Tensor scale_V,
+                                                 bool is_causal, bool quant) {
     TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
     TORCH_CHECK(Q.dtype() == torch::kInt8, "Q must be int8");
     TORCH_CHECK(K.dtype() == torch::kInt8, "K must be int8");
@@ -88,6 +91,19 @@ torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, tor
     auto sV = scale_V.contiguous().view({n_tokens});
     auto q = aligned_i8(Q), k = aligned_i8(K), v = aligned_i8(V);
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
+    if (quant) {
+        auto oq = torch::empty({batch, heads, seq_len, head_dim},
+                               torch::TensorOptions().dtype(torch::kInt8).device(Q.device()));
+        auto os = torch::empty({batch, heads, seq_len},
+                               torch::TensorOptions().dtype(torch::kFloat32).device(Q.device()));
+        check_status(int8k_attention_forward_quant(
+                         q.data_ptr<int8_t>(), k.data_ptr<int8_t>(), v.data_ptr<int8_t>(),
+                         oq.data_ptr<int8_t>(), os.data_ptr<float>(), sQ.data_ptr<float>(),
+                         sK.data_ptr<float>(), sV.data_ptr<float>(), (int)batch, (int)heads,
+                         (int)seq_len, (int)head_dim, is_causal ? 1 : 0, current_stream(Q)),
+                     "int8_attention_forward_quant");
+        return {oq, os};
+    }
     auto out = torch::empty({batch, heads, seq_len, head_dim},
                             torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const int st = int8k_attention_forward(
@@ -96,7 +112,20 @@ torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, tor
         sK.data_ptr<float>(), sV.data_ptr<float>(), (int)batch, (int)heads, (int)seq_len,
         (int)head_dim, is_causal ? 1 : 0, current_stream(Q));
     check_status(st, "int8_attention_forward");
-    return out;
+    return {out};
+}
+
+torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                           torch::Tensor scale_Q, torch::Tensor scale_K,
+                                           torch::Tensor scale_V, bool is_causal) {
+    return attention_impl(Q, K, V, scale_Q, scale_K, scale_V, is_causal, false)[0];
+}
+
+std::tuple<torch::Tensor, torch::Tensor> int8_attention_forward_quant_torch(
+    torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor scale_Q,
+    torch::Tensor scale_K, torch::Tensor scale_V, bool is_causal) {
+    auto r = attention_impl(Q, K, V, scale_Q, scale_K, scale_V, is_causal, true);
+    return {r[0], r[1]};
 }
 
 // ── decode attention (seq_q == 1) ─────────────────────────────────────────
@@ -104,9 +133,10 @@ torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, tor
 // Q : (batch, heads, head_dim) int8; K, V : (batch, heads, seq_kv, head_dim)
 // int8; scale_Q numel batch*heads; scale_K/V numel batch*heads*seq_kv (fp32).
 // Returns (batch, heads, head_dim) fp16.
-torch::Tensor int8_decode_attention_forward_torch(torch::Tensor Q, torch::Tensor K,
-                                                  torch::Tensor V, torch::Tensor scale_Q,
-                                                  torch::Tensor scale_K, torch::Tensor scale_V) {
+// With `quant`: {int8 (batch, heads, head_dim), fp32 scales (batch, heads)}.
+static std::vector<torch::Tensor> decode_impl(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                              torch::Tensor scale_Q, torch::Tensor scale_K,
+                                              torch::Tensor scale_V, bool quant) {
     TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
     TORCH_CHECK(Q.dtype() == torch::kInt8, "Q must be int8");
     TORCH_CHECK(K.dtype() == torch::kInt8 && V.dtype() == torch::kInt8, "K, V must be int8");
@@ -142,18 +172,44 @@ torch::Tensor int8_decode_attention_forward_torch(torch::Tensor Q, torch::Tensor
     auto q = aligned_i8(Q), k = aligned_i8(K), v = aligned_i8(V);
 
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
-    auto out = torch::empty({batch, heads, head_dim},
-                            torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const size_t ws_bytes =
         int8k_decode_attention_workspace_bytes((int)BH, (int)seq_kv, (int)head_dim, 0);
     auto ws = workspace(ws_bytes, Q.device());
+    if (quant) {
+        auto oq = torch::empty({batch, heads, head_dim},
+                               torch::TensorOptions().dtype(torch::kInt8).device(Q.device()));
+        auto os = torch::empty({batch, heads},
+                               torch::TensorOptions().dtype(torch::kFloat32).device(Q.device()));
+        check_status(int8k_decode_attention_forward_quant(
+                         q.data_ptr<int8_t>(), k.data_ptr<int8_t>(), v.data_ptr<int8_t>(),
+                         oq.data_ptr<int8_t>(), os.data_ptr<float>(), sQ.data_ptr<float>(),
+                         sK.data_ptr<float>(), sV.data_ptr<float>(), (int)BH, (int)seq_kv,
+                         (int)head_dim, 0, ws.data_ptr(), ws_bytes, current_stream(Q)),
+                     "int8_decode_attention_forward_quant");
+        return {oq, os};
+    }
+    auto out = torch::empty({batch, heads, head_dim},
+                            torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const int st = int8k_decode_attention_forward(
         q.data_ptr<int8_t>(), k.data_ptr<int8_t>(), v.data_ptr<int8_t>(),
         reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
         sK.data_ptr<float>(), sV.data_ptr<float>(), (int)BH, (int)seq_kv, (int)head_dim, 0,
         ws.data_ptr(), ws_bytes, current_stream(Q));
     check_status(st, "int8_decode_attention_forward");
-    return out;
+    return {out};
+}
+
+torch::Tensor int8_decode_attention_forward_torch(torch::Tensor Q, torch::Tensor K,
+                                                  torch::Tensor V, torch::Tensor scale_Q,
+                                                  torch::Tensor scale_K, torch::Tensor scale_V) {
+    return decode_impl(Q, K, V, scale_Q, scale_K, scale_V, false)[0];
+}
+
+std::tuple<torch::Tensor, torch::Tensor> int8_decode_attention_forward_quant_torch(
+    torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor scale_Q,
+    torch::Tensor scale_K, torch::Tensor scale_V) {
+    auto r = decode_impl(Q, K, V, scale_Q, scale_K, scale_V, true);
+    return {r[0], r[1]};
 }
 
 // ── INT8 MLP ────────────────────────────────────────────────────────────────
@@ -543,10 +599,11 @@ void kv_cache_append_torch(torch::Tensor k_new, torch::Tensor v_new, torch::Tens
 
 // Decode over the first seq_len positions of a preallocated cache
 // (batch, heads, capacity, head_dim); Q (batch, heads, head_dim) int8.
-torch::Tensor int8_decode_attention_forward_cache_torch(torch::Tensor Q, torch::Tensor K_cache,
-                                                        torch::Tensor V_cache, torch::Tensor scale_Q,
-                                                        torch::Tensor sK_cache,
-                                                        torch::Tensor sV_cache, int64_t seq_len) {
+static std::vector<torch::Tensor> decode_cache_impl(torch::Tensor Q, torch::Tensor K_cache,
+                                                    torch::Tensor V_cache, torch::Tensor scale_Q,
+                                                    torch::Tensor sK_cache,
+                                                    torch::Tensor sV_cache, int64_t seq_len,
+                                                    bool quant) {
     TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
     TORCH_CHECK(Q.dtype() == torch::kInt8 && K_cache.dtype() == torch::kInt8 &&
                     V_cache.dtype() == torch::kInt8,
@@ -570,26 +627,52 @@ torch::Tensor int8_decode_attention_forward_cache_torch(torch::Tensor Q, torch::
     auto sK = sK_cache.contiguous();
     auto sV = sV_cache.contiguous();
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
-    auto out = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const int BH = (int)(B * H);
     const size_t ws_bytes = int8k_decode_attention_workspace_bytes(BH, (int)seq_len, (int)D, 0);
     auto ws = workspace(ws_bytes, Q.device());
+    if (quant) {
+        auto oq = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kInt8).device(Q.device()));
+        auto os = torch::empty({B, H}, torch::TensorOptions().dtype(torch::kFloat32).device(Q.device()));
+        check_status(int8k_decode_attention_forward_cache_quant(
+                         Q.data_ptr<int8_t>(), K_cache.data_ptr<int8_t>(),
+                         V_cache.data_ptr<int8_t>(), oq.data_ptr<int8_t>(), os.data_ptr<float>(),
+                         sQ.data_ptr<float>(), sK.data_ptr<float>(), sV.data_ptr<float>(), BH,
+                         (int)seq_len, (int)cap, (int)D, 0, ws.data_ptr(), ws_bytes,
+                         current_stream(Q)),
+                     "int8_decode_attention_forward_cache_quant");
+        return {oq, os};
+    }
+    auto out = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const int st = int8k_decode_attention_forward_cache(
         Q.data_ptr<int8_t>(), K_cache.data_ptr<int8_t>(), V_cache.data_ptr<int8_t>(),
         reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
         sK.data_ptr<float>(), sV.data_ptr<float>(), BH, (int)seq_len, (int)cap, (int)D, 0,
         ws.data_ptr(), ws_bytes, current_stream(Q));
     check_status(st, "int8_decode_attention_forward_cache");
-    return out;
+    return {out};
+}
+
+torch::Tensor int8_decode_attention_forward_cache_torch(torch::Tensor Q, torch::Tensor K_cache,
+                                                        torch::Tensor V_cache, torch::Tensor scale_Q,
+                                                        torch::Tensor sK_cache,
+                                                        torch::Tensor sV_cache, int64_t seq_len) {
+    return decode_cache_impl(Q, K_cache, V_cache, scale_Q, sK_cache, sV_cache, seq_len, false)[0];
+}
+
+std::tuple<torch::Tensor, torch::Tensor> int8_decode_attention_forward_cache_quant_torch(
+    torch::Tensor Q, torch::Tensor K_cache, torch::Tensor V_cache, torch::Tensor scale_Q,
+    torch::Tensor sK_cache, torch::Tensor sV_cache, int64_t seq_len) {
+    auto r = decode_cache_impl(Q, K_cache, V_cache, scale_Q, sK_cache, sV_cache, seq_len, true);
+    return {r[0], r[1]};
 }
 
 // Decode over a paged int8 KV cache (no reference counterpart): K/V pages
 // [num_pages, H, page, D], scale pages [num_pages, H, page], block_tables
 // [B, max_pages] int32, context_lens [B] int32 (each in [1, max_context]).
-torch::Tensor int8_decode_attention_forward_paged_torch(
+static std::vector<torch::Tensor> decode_paged_impl(
     torch::Tensor Q, torch::Tensor K_pages, torch::Tensor V_pages, torch::Tensor scale_Q,
     torch::Tensor sK_pages, torch::Tensor sV_pages, torch::Tensor block_tables,
-    torch::Tensor context_lens, int64_t max_context) {
+    torch::Tensor context_lens, int64_t max_context, bool quant) {
     TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
     TORCH_CHECK(Q.dtype() == torch::kInt8 && K_pages.dtype() == torch::kInt8 &&
                     V_pages.dtype() == torch::kInt8,
@@ -621,10 +704,23 @@ torch::Tensor int8_decode_attention_forward_paged_torch(
     auto bt = block_tables.contiguous();
     auto cl = context_lens.contiguous();
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
-    auto out = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const size_t ws_bytes = int8k_decode_attention_paged_workspace_bytes(
         (int)B, (int)H, (int)max_context, (int)D, 0);
     auto ws = workspace(ws_bytes, Q.device());
+    if (quant) {
+        auto oq = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kInt8).device(Q.device()));
+        auto os = torch::empty({B, H}, torch::TensorOptions().dtype(torch::kFloat32).device(Q.device()));
+        check_status(int8k_decode_attention_forward_paged_quant(
+                         Q.data_ptr<int8_t>(), K_pages.data_ptr<int8_t>(),
+                         V_pages.data_ptr<int8_t>(), oq.data_ptr<int8_t>(), os.data_ptr<float>(),
+                         sQ.data_ptr<float>(), sK.data_ptr<float>(), sV.data_ptr<float>(),
+                         bt.data_ptr<int32_t>(), cl.data_ptr<int32_t>(), (int)B, (int)H, (int)D,
+                         (int)NP, (int)P, (int)max_pages, (int)max_context, 0, ws.data_ptr(),
+                         ws_bytes, current_stream(Q)),
+                     "int8_decode_attention_forward_paged_quant");
+        return {oq, os};
+    }
+    auto out = torch::empty({B, H, D}, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const int st = int8k_decode_attention_forward_paged(
         Q.data_ptr<int8_t>(), K_pages.data_ptr<int8_t>(), V_pages.data_ptr<int8_t>(),
         reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
@@ -632,7 +728,24 @@ torch::Tensor int8_decode_attention_forward_paged_torch(
         cl.data_ptr<int32_t>(), (int)B, (int)H, (int)D, (int)NP, (int)P, (int)max_pages,
         (int)max_context, 0, ws.data_ptr(), ws_bytes, current_stream(Q));
     check_status(st, "int8_decode_attention_forward_paged");
-    return out;
+    return {out};
+}
+
+torch::Tensor int8_decode_attention_forward_paged_torch(
+    torch::Tensor Q, torch::Tensor K_pages, torch::Tensor V_pages, torch::Tensor scale_Q,
+    torch::Tensor sK_pages, torch::Tensor sV_pages, torch::Tensor block_tables,
+    torch::Tensor context_lens, int64_t max_context) {
+    return decode_paged_impl(Q, K_pages, V_pages, scale_Q, sK_pages, sV_pages, block_tables,
+                             context_lens, max_context, false)[0];
+}
+
+std::tuple<torch::Tensor, torch::Tensor> int8_decode_attention_forward_paged_quant_torch(
+    torch::Tensor Q, torch::Tensor K_pages, torch::Tensor V_pages, torch::Tensor scale_Q,
+    torch::Tensor sK_pages, torch::Tensor sV_pages, torch::Tensor block_tables,
+    torch::Tensor context_lens, int64_t max_context) {
+    auto r = decode_paged_impl(Q, K_pages, V_pages, scale_Q, sK_pages, sV_pages, block_tables,
+                               context_lens, max_context, true);
+    return {r[0], r[1]};
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -685,5 +798,19 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "INT8 decode attention over a paged KV cache (block tables, per-sequence lengths)");
     m.def("int8_decode_attention_forward_cache", &int8_decode_attention_forward_cache_torch,
           "INT8 decode attention over the first seq_len positions of a KV cache — returns FP16");
+    // The attention output emitted as int8 + per-token scales (the per-token
+    // quantization of the fp16 rows the ops above return).
+    m.def("int8_attention_forward_quant", &int8_attention_forward_quant_torch,
+          "INT8 attention emitting per-token int8 — returns (int8, fp32 scales)",
+          py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("scale_Q"), py::arg("scale_K"),
+          py::arg("scale_V"), py::arg("is_causal") = false);
+    m.def("int8_decode_attention_forward_quant", &int8_decode_attention_forward_quant_torch,
+          "INT8 decode attention emitting per-token int8 — returns (int8, fp32 scales)");
+    m.def("int8_decode_attention_forward_cache_quant",
+          &int8_decode_attention_forward_cache_quant_torch,
+          "INT8 decode over a KV cache emitting per-token int8 — returns (int8, fp32 scales)");
+    m.def("int8_decode_attention_forward_paged_quant",
+          &int8_decode_attention_forward_paged_quant_torch,
+          "INT8 paged decode emitting per-token int8 — returns (int8, fp32 scales)");
     m.attr("abi_version") = int8k_abi_version();
 }

@@ -21,9 +21,16 @@
 // registers it was computed in; V is staged once per tile into LDS as fp16 V^T
 // with the key order permuted to match those P^T registers, so each V^T
 // fragment is a single 16-byte LDS read.
+//
+// With an int8 destination the epilogue emits the per-token quantization of
+// the fp16 output row instead (the attention output as the next INT8 stage's
+// input): the fp16 values the fp16 path would store, their row absmax, and
+// the per-token quantizer's codes and scale — the same bytes as
+// int8k_quantize_per_token over the fp16 output, without its round trip.
 #include <cmath>
 
 #include "int8k_common.h"
+#include "rows.h"
 
 namespace int8k {
 namespace {
@@ -198,7 +205,8 @@ template <int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
     const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
-    uint16_t* __restrict__ out, int S, int n_qtiles, float qk_scale_log2) {
+    uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qout_scale, int S,
+    int n_qtiles, float qk_scale_log2) {
     constexpr int NS = D / 32;  // 32-wide d slices (QK k-steps) and O^T row tiles
     using St = Stage<D>;
     extern __shared__ __align__(16) char smem[];
@@ -411,26 +419,52 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
     }
 
     const float L = sum_xor32(lsum);
-    if (!qok) return;
+    if (!qok) return;  // lanes l and l^32 share q, so both leave or both stay
     const float inv = 1.f / L;
+    // fp16 output values (rounded from the fp32 quotient); lane l holds
+    // d = 32 t + 8 g + 4 h + c of its query, lane l^32 the other half
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = __half2float(f16_of_f32(o[t][r] * inv));
+    if (qout != nullptr) {
+        float am = 0.f;
+#pragma unroll
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) am = fmaxf(am, fabsf(o[t][r]));
+        am = max_xor32(am);
+        const float sc = fmaxf(am, 1e-8f) / 127.f;
+        const float rinv = 1.f / sc;
+        int8_t* qrow = qout + (base + q) * D;
+#pragma unroll
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float y[4] = {o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]};
+                store_codes<4>(y, sc, rinv, qrow + 32 * t + 8 * g + 4 * h);
+            }
+        if (h == 0) qout_scale[base + q] = sc;
+        return;
+    }
     uint16_t* orow = out + (base + q) * D;
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = 32 * t + 8 * g + 4 * h;
-            const uint32_t lo = f32_to_f16_bits(o[t][4 * g] * inv) |
-                                ((uint32_t)f32_to_f16_bits(o[t][4 * g + 1] * inv) << 16);
-            const uint32_t hi = f32_to_f16_bits(o[t][4 * g + 2] * inv) |
-                                ((uint32_t)f32_to_f16_bits(o[t][4 * g + 3] * inv) << 16);
+            const uint32_t lo = f32_to_f16_bits(o[t][4 * g]) |
+                                ((uint32_t)f32_to_f16_bits(o[t][4 * g + 1]) << 16);
+            const uint32_t hi = f32_to_f16_bits(o[t][4 * g + 2]) |
+                                ((uint32_t)f32_to_f16_bits(o[t][4 * g + 3]) << 16);
             *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
         }
 }
 
 template <int D>
 int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
-                   const float* sQ, const float* sK, const float* sV, int BH, int S, bool causal,
-                   hipStream_t stream) {
+                   int8_t* qout, float* qscale, const float* sQ, const float* sK, const float* sV,
+                   int BH, int S, bool causal, hipStream_t stream) {
     const int n_qtiles = (S + kQ - 1) / kQ;
     const long long blocks = (long long)BH * n_qtiles;
     const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
@@ -450,11 +484,42 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
     }
     if (causal)
         prefill_kernel<D, true><<<(unsigned)blocks, kThreads, lds, stream>>>(
-            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk);
+            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk);
     else
         prefill_kernel<D, false><<<(unsigned)blocks, kThreads, lds, stream>>>(
-            Q, K, V, sQ, sK, sV, out, S, n_qtiles, qk);
+            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk);
     return check_launch("prefill_kernel");
+}
+
+// Shared checks and dispatch of both entry points: exactly one of out
+// (fp16) and qout/qscale (int8 + per-token scale) is set.
+int prefill_entry(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out, int8_t* qout,
+                  float* qscale, const float* scale_Q, const float* scale_K, const float* scale_V,
+                  int batch, int heads, int seq_len, int head_dim, int causal, void* stream) {
+    if (!Q || !K || !V || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
+    const long long BH = (long long)batch * heads;
+    if (BH * ((seq_len + kQ - 1) / kQ) * kThreads >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
+    if ((long long)seq_len * head_dim >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;  // buffer range
+    if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) ||
+        !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
+        return INT8K_ERR_MISALIGNED;
+    if (out ? !aligned_to(out, 8) : !(aligned_to(qout, 4) && aligned_to(qscale, 4)))
+        return INT8K_ERR_MISALIGNED;
+    hipStream_t s = as_stream(stream);
+    const bool c = causal != 0;
+    switch (head_dim) {
+        case 64:
+            return launch_prefill<64>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
+                                      (int)BH, seq_len, c, s);
+        case 128:
+            return launch_prefill<128>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
+                                       (int)BH, seq_len, c, s);
+        default:
+            return launch_prefill<256>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
+                                       (int)BH, seq_len, c, s);
+    }
 }
 
 }  // namespace
@@ -467,19 +532,19 @@ extern "C" int int8k_attention_forward(const int8_t* Q, const int8_t* K, const i
                                        const float* scale_V, int batch, int heads, int seq_len,
                                        int head_dim, int causal, void* stream) {
     clear_last_error();
-    if (!Q || !K || !V || !out || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
-    if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
-    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
-    const long long BH = (long long)batch * heads;
-    if (BH * ((seq_len + kQ - 1) / kQ) * kThreads >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
-    if ((long long)seq_len * head_dim >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;  // buffer range
-    if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) || !aligned_to(out, 8) ||
-        !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
-        return INT8K_ERR_MISALIGNED;
-    hipStream_t s = as_stream(stream);
-    switch (head_dim) {
-        case 64: return launch_prefill<64>(Q, K, V, out, scale_Q, scale_K, scale_V, (int)BH, seq_len, causal != 0, s);
-        case 128: return launch_prefill<128>(Q, K, V, out, scale_Q, scale_K, scale_V, (int)BH, seq_len, causal != 0, s);
-        default: return launch_prefill<256>(Q, K, V, out, scale_Q, scale_K, scale_V, (int)BH, seq_len, causal != 0, s);
-    }
+    if (!out) return INT8K_ERR_INVALID_ARGUMENT;
+    return prefill_entry(Q, K, V, out, nullptr, nullptr, scale_Q, scale_K, scale_V, batch, heads,
+                         seq_len, head_dim, causal, stream);
+}
+
+extern "C" int int8k_attention_forward_quant(const int8_t* Q, const int8_t* K, const int8_t* V,
+                                             int8_t* out_q, float* out_scale,
+                                             const float* scale_Q, const float* scale_K,
+                                             const float* scale_V, int batch, int heads,
+                                             int seq_len, int head_dim, int causal,
+                                             void* stream) {
+    clear_last_error();
+    if (!out_q || !out_scale) return INT8K_ERR_INVALID_ARGUMENT;
+    return prefill_entry(Q, K, V, nullptr, out_q, out_scale, scale_Q, scale_K, scale_V, batch,
+                         heads, seq_len, head_dim, causal, stream);
 }

@@ -56,6 +56,10 @@ _SIGNATURES = {
     "int8k_quantize_heads": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "int8k_decode_attention_forward_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                                   _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "int8k_attention_forward_quant": (_I, [_P] * 8 + [_I] * 5 + [_P]),
+    "int8k_decode_attention_forward_quant": (_I, [_P] * 8 + [_I] * 4 + [_P, _SZ, _P]),
+    "int8k_decode_attention_forward_cache_quant": (_I, [_P] * 8 + [_I] * 5 + [_P, _SZ, _P]),
+    "int8k_decode_attention_forward_paged_quant": (_I, [_P] * 10 + [_I] * 8 + [_P, _SZ, _P]),
 }
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
@@ -144,6 +148,22 @@ def decode_attention(Qi, Ki, Vi, sQ, sK, sV, nsplit: int = 0, out=None, workspac
     return out
 
 
+def decode_attention_quant(Qi, Ki, Vi, sQ, sK, sV, nsplit: int = 0):
+    """As decode_attention, emitting (int8 [BH,D], fp32 scales [BH])."""
+    import torch
+
+    BH, D = Qi.shape[0], Qi.shape[-1]
+    S = Ki.numel() // (BH * D)
+    q, s, _ = _quant_rows((BH, D), Qi.device)
+    ws = torch.empty(max(decode_workspace_bytes(BH, S, D, nsplit), 1), dtype=torch.uint8,
+                     device=Qi.device)
+    st = load().int8k_decode_attention_forward_quant(
+        _ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(q), _ptr(s), _ptr(sQ), _ptr(sK), _ptr(sV),
+        BH, S, D, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
+    check("int8k_decode_attention_forward_quant", st)
+    return q, s
+
+
 # --------------------------------------------------------------------------
 # MLP / GEMM
 # --------------------------------------------------------------------------
@@ -221,6 +241,28 @@ def attention_forward(Qi, Ki, Vi, sQ, sK, sV, causal=False, out=None):
                                         _stream(Qi))
     check("int8k_attention_forward", st)
     return out
+
+
+def _quant_rows(shape, device):
+    import torch
+
+    n = 1
+    for d in shape[:-1]:
+        n *= d
+    return (torch.empty(shape, dtype=torch.int8, device=device),
+            torch.empty(shape[:-1], dtype=torch.float32, device=device), n)
+
+
+def attention_forward_quant(Qi, Ki, Vi, sQ, sK, sV, causal=False):
+    """As attention_forward, emitting the per-token int8 of the fp16 output:
+    (int8 [B,H,S,D], fp32 scales [B,H,S])."""
+    B, H, S, D = Qi.shape
+    q, s, _ = _quant_rows((B, H, S, D), Qi.device)
+    st = load().int8k_attention_forward_quant(_ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(q), _ptr(s),
+                                              _ptr(sQ), _ptr(sK), _ptr(sV), B, H, S, D,
+                                              int(bool(causal)), _stream(Qi))
+    check("int8k_attention_forward_quant", st)
+    return q, s
 
 
 # --------------------------------------------------------------------------
@@ -317,6 +359,22 @@ def decode_attention_cache(Qi, K_cache, V_cache, sQ, sK_cache, sV_cache, S, nspl
     return out
 
 
+def decode_attention_cache_quant(Qi, K_cache, V_cache, sQ, sK_cache, sV_cache, S, nsplit=0):
+    """As decode_attention_cache, emitting (int8 [BH,D], fp32 scales [BH])."""
+    import torch
+
+    B, H, cap, D = K_cache.shape
+    BH = B * H
+    q, s, _ = _quant_rows((BH, D), Qi.device)
+    ws = torch.empty(max(decode_workspace_bytes(BH, S, D, nsplit), 1), dtype=torch.uint8,
+                     device=Qi.device)
+    st = load().int8k_decode_attention_forward_cache_quant(
+        _ptr(Qi), _ptr(K_cache), _ptr(V_cache), _ptr(q), _ptr(s), _ptr(sQ), _ptr(sK_cache),
+        _ptr(sV_cache), BH, S, cap, D, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
+    check("int8k_decode_attention_forward_cache_quant", st)
+    return q, s
+
+
 def decode_paged_workspace_bytes(B, H, max_context, D, nsplit=0):
     return load().int8k_decode_attention_paged_workspace_bytes(B, H, max_context, D, nsplit)
 
@@ -340,6 +398,24 @@ def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_t
         max_pages, max_context, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
     check("int8k_decode_attention_forward_paged", st)
     return out
+
+
+def decode_attention_paged_quant(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_tables,
+                                 context_lens, max_context, nsplit=0):
+    """As decode_attention_paged, emitting (int8 [B,H,D], fp32 scales [B,H])."""
+    import torch
+
+    num_pages, H, page, D = K_pages.shape
+    B, max_pages = block_tables.shape
+    q, s, _ = _quant_rows((B, H, D), Qi.device)
+    ws = torch.empty(max(decode_paged_workspace_bytes(B, H, max_context, D, nsplit), 1),
+                     dtype=torch.uint8, device=Qi.device)
+    st = load().int8k_decode_attention_forward_paged_quant(
+        _ptr(Qi), _ptr(K_pages), _ptr(V_pages), _ptr(q), _ptr(s), _ptr(sQ), _ptr(sK_pages),
+        _ptr(sV_pages), _ptr(block_tables), _ptr(context_lens), B, H, D, num_pages, page,
+        max_pages, max_context, nsplit, _ptr(ws), ws.numel(), _stream(Qi))
+    check("int8k_decode_attention_forward_paged_quant", st)
+    return q, s
 
 
 def layernorm_quantize_per_token(x, gamma=None, beta=None, eps=1e-5, want_y=False):

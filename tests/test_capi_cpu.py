@@ -125,6 +125,35 @@ def test_quant_argument_validation(capi):
         None) == capi.INT8K_ERR_INVALID_ARGUMENT
 
 
+def test_quantized_attention_output_validation(capi):
+    # the int8-output entry points: both outputs required, scale output 4-byte aligned,
+    # the rest of the checks shared with the fp16 entry points
+    lib = capi.load()
+    F = _fake
+    pre = lambda q=0x40000, s=0x48000, D=128: lib.int8k_attention_forward_quant(  # noqa: E731
+        F(0x10000), F(0x20000), F(0x30000), F(q), F(s), F(0x50000), F(0x60000), F(0x70000),
+        1, 2, 64, D, 1, None)
+    assert pre(q=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert pre(s=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert pre(s=0x48002) == capi.INT8K_ERR_MISALIGNED
+    assert pre(D=96) == capi.INT8K_ERR_UNSUPPORTED
+    dec = lambda q=0x40000, s=0x48000, ws_bytes=1 << 30: (  # noqa: E731
+        lib.int8k_decode_attention_forward_quant(
+            F(0x10000), F(0x20000), F(0x30000), F(q), F(s), F(0x50000), F(0x60000), F(0x70000),
+            4, 100, 128, 0, F(0x80000), ws_bytes, None))
+    assert dec(q=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert dec(s=0x48001) == capi.INT8K_ERR_MISALIGNED
+    assert dec(ws_bytes=capi.decode_workspace_bytes(4, 100, 128) - 1) == capi.INT8K_ERR_WORKSPACE
+    assert lib.int8k_decode_attention_forward_cache_quant(
+        F(0x10000), F(0x20000), F(0x30000), F(0x40000), F(0), F(0x50000), F(0x60000),
+        F(0x70000), 4, 100, 90, 128, 0, F(0x80000), 1 << 30, None) == \
+        capi.INT8K_ERR_INVALID_ARGUMENT
+    assert lib.int8k_decode_attention_forward_paged_quant(
+        F(0x10000), F(0x20000), F(0x30000), F(0), F(0x48000), F(0x50000), F(0x60000),
+        F(0x70000), F(0x80000), F(0x90000), 2, 4, 128, 8, 16, 4, 64, 0, F(0xa0000), 1 << 30,
+        None) == capi.INT8K_ERR_INVALID_ARGUMENT
+
+
 def test_paged_decode_argument_validation(capi):
     lib = capi.load()
     F = _fake
