@@ -412,6 +412,136 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __r
         p.pmax[(size_t)blockIdx.x * M + row] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// ---------------------------------------------------------------- few tokens
+// Skinny GEMM for small GEMMs (decode-time MLPs): a block owns one 32 x 32
+// output tile (grid = N/32 column blocks x M/32 row blocks) over the whole K,
+// and its four waves take a quarter of K each.  MFMA operands come straight
+// from global memory: the tile's 32 rows of A and 32 rows of Bt, 16 bytes per
+// lane, two groups of four 32-deep k slices in flight.  The four int32
+// partial tiles meet in LDS and the block's 256 threads apply the epilogue,
+// writing one absmax partial per (32-column block, row).  No partial sums
+// leave the chip; split-K over blocks (above) would write them to memory.
+// Rows past M read row M-1 and are not stored.
+//
+//
+// It runs at ~3 us + 7 us per 2^30 multiply-adds on MI355X (latency-bound
+// loads; the tiles re-read A and Bt through L2, ~MNK/16 bytes).  Per GEMM,
+// measured against split-K and the 256 x 256 kernel at d_model 512..4096 and
+// T 1..2048, it wins up to M N K = 2^31, and up to 2^32 above 512 rows (no
+// split-K there) when the 256 x 256 grid would have fewer than 64 tiles.
+constexpr int kSkinnyN = 32;
+constexpr int kSkinnyLds = 4 * 32 * kSkinnyN * 4 + 32 * 4;  // partials, row scales
+
+inline bool use_skinny(int M, int N, int K) {
+    if (N % kSkinnyN != 0 || K % 512 != 0) return false;
+    const long long mnk = (long long)M * N * K;
+    const long long big_tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    return mnk <= (1LL << 31) || (M > 4 * kSkM && big_tiles < 64 && mnk <= (1LL << 32));
+}
+
+// Absmax partials per row that the GEMM's epilogue leaves (requant reads them).
+inline int epi_tiles(int M, int N, int K) {
+    return use_skinny(M, N, K) ? N / kSkinnyN : (N + BN - 1) / BN;
+}
+
+__device__ __forceinline__ void skinny_load(v4i (&b)[4], v4i (&a)[4], const int8_t* arow,
+                                            const int8_t* brow, int k) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        b[u] = *reinterpret_cast<const v4i*>(brow + k + 32 * u);
+        a[u] = *reinterpret_cast<const v4i*>(arow + k + 32 * u);
+    }
+}
+
+__device__ __forceinline__ void skinny_mfma(v16i& acc, const v4i (&b)[4], const v4i (&a)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u], b[u], acc, 0, 0, 0);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_i8_skinny_kernel(const int8_t* __restrict__ A,
+                                                             const int8_t* __restrict__ Bt,
+                                                             int M, int N, int K, EpiParams p) {
+    extern __shared__ __align__(16) char lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * kSkinnyN;
+    const int m0 = blockIdx.y * 32;
+    const int c = threadIdx.x & 31;
+    const int col = n0 + c;
+    // epilogue operands first, so the K loop hides their latency
+    const float pre_sa = p.sa[(size_t)min(m0 + c, M - 1) * p.sa_stride];
+    const float sb = p.sb[(size_t)col * p.sb_stride];
+    const float bias = p.bias != nullptr ? p.bias[col] : 0.f;
+
+    const int kq = K / 4;  // this wave's quarter of K, a multiple of 128
+    const int koff = wave * kq + (lane >> 5) * 16;
+    const int8_t* arow = A + (size_t)min(m0 + (lane & 31), M - 1) * K + koff;
+    const int8_t* brow = Bt + (size_t)(n0 + (lane & 31)) * K + koff;
+    v16i acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0;
+    // two groups of four k slices in flight: group g+1 loads while g runs
+    v4i b0[4], a0[4], b1[4], a1[4];
+    skinny_load(b0, a0, arow, brow, 0);
+    for (int k = 0; k < kq; k += 256) {
+        if (k + 128 < kq) skinny_load(b1, a1, arow, brow, k + 128);
+        skinny_mfma(acc, b0, a0);
+        if (k + 128 >= kq) break;
+        if (k + 256 < kq) skinny_load(b0, a0, arow, brow, k + 256);
+        skinny_mfma(acc, b1, a1);
+    }
+    // partials part[wave][row][col] (row acc_row(r), column lane % 32), row scales
+    int* part = reinterpret_cast<int*>(lds);
+    float* esa = reinterpret_cast<float*>(lds + 4 * 32 * kSkinnyN * 4);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[(wave * 32 + acc_row(r, lane)) * kSkinnyN + (lane & 31)] = acc[r];
+    if (threadIdx.x < 32) esa[threadIdx.x] = pre_sa;
+    __syncthreads();
+    // epilogue: thread t takes column t % 32 of rows t / 32 + 8 j (j < 4); the
+    // 32 lanes of a half-wave share a row: its absmax by DPP inside each 16-lane
+    // row and v_permlane16_swap across the two (VALU only)
+    float v[4];
+    int mx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int rl = (threadIdx.x >> 5) + 8 * j;
+        const int s = part[rl * kSkinnyN + c] + part[(32 + rl) * kSkinnyN + c] +
+                      part[(64 + rl) * kSkinnyN + c] + part[(96 + rl) * kSkinnyN + c];
+        v[j] = epi_value<EPI>(s, esa[rl], sb, bias);
+        mx[j] = __float_as_int(fabsf(v[j]));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx[j] = max(mx[j], dpp_xor1(mx[j]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx[j] = max(mx[j], dpp_xor2(mx[j]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx[j] = max(mx[j], dpp_half_mirror(mx[j]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx[j] = max(mx[j], dpp_row_mirror(mx[j]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(mx[j], mx[j], false, false);
+        mx[j] = max((int)sw[0], (int)sw[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = m0 + (threadIdx.x >> 5) + 8 * j;
+        if (row < M) {
+            p.c16[(size_t)row * p.ldc + col] = f32_to_f16_bits(v[j]);
+            if (c == 0) p.pmax[(size_t)blockIdx.x * M + row] = __int_as_float(mx[j]);
+        }
+    }
+}
+
+template <int EPI>
+int launch_gemm_skinny(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
+                       hipStream_t stream) {
+    const dim3 grid(N / kSkinnyN, (M + 31) / 32);
+    gemm_i8_skinny_kernel<EPI><<<grid, 256, kSkinnyLds, stream>>>(A, Bt, M, N, K, p);
+    return check_launch("gemm_i8_skinny_kernel");
+}
+
 // Split plan for an M x N x K GEMM: run split-K when the 256 x 256 grid would
 // have fewer tiles than the device has CUs (256 on MI355X).
 struct SplitKPlan {
@@ -580,12 +710,13 @@ MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
     w.h16 = reinterpret_cast<uint16_t*>(take((size_t)T * dff * 2));
     w.hq = reinterpret_cast<int8_t*>(take((size_t)T * dff));
     w.sh = reinterpret_cast<float*>(take((size_t)T * 4));
-    w.p1 = reinterpret_cast<float*>(take((size_t)((dff + BN - 1) / BN) * T * 4));
+    w.p1 = reinterpret_cast<float*>(take((size_t)epi_tiles(T, dff, dm) * T * 4));
     w.o16 = reinterpret_cast<uint16_t*>(take((size_t)T * dm * 2));
-    w.p2 = reinterpret_cast<float*>(take((size_t)((dm + BN - 1) / BN) * T * 4));
+    w.p2 = reinterpret_cast<float*>(take((size_t)epi_tiles(T, dm, dff) * T * 4));
     w.tmax = reinterpret_cast<float*>(take(4));
-    w.part = reinterpret_cast<int32_t*>(take(std::max(splitk_partial_bytes(T, dff, dm),
-                                                      splitk_partial_bytes(T, dm, dff))));
+    const size_t part1 = use_skinny(T, dff, dm) ? 0 : splitk_partial_bytes(T, dff, dm);
+    const size_t part2 = use_skinny(T, dm, dff) ? 0 : splitk_partial_bytes(T, dm, dff);
+    w.part = reinterpret_cast<int32_t*>(take(std::max(part1, part2)));
     w.bytes = off;
     return w;
 }
@@ -691,14 +822,16 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p1.bias = bias1;
     p1.pmax = w.p1;
     const SplitKPlan sk1 = splitk_plan(T, d_ff, d_model);
-    if (sk1.use)
+    if (use_skinny(T, d_ff, d_model))
+        st = launch_gemm_skinny<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
+    else if (sk1.use)
         st = launch_gemm_splitk<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, sk1, w.part, p1, s);
     else
         st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     if (st != INT8K_OK) return st;
-    // per-token requant of the hidden (either path leaves one absmax partial per
-    // 256 columns and row)
-    const int tn1 = (d_ff + BN - 1) / BN;
+    // per-token requant of the hidden (one absmax partial per row and 256-column
+    // tile, or per 32-column block of the skinny path)
+    const int tn1 = epi_tiles(T, d_ff, d_model);
     requant_rows_kernel<<<T, 256, 0, s>>>(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T,
                                           d_ff);
     if ((st = check_launch("requant_rows_kernel")) != INT8K_OK) return st;
@@ -712,12 +845,14 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p2.sb_stride = n_scale_W2 == 1 ? 0 : 1;
     p2.pmax = w.p2;
     const SplitKPlan sk2 = splitk_plan(T, d_model, d_ff);
-    if (sk2.use)
+    if (use_skinny(T, d_model, d_ff))
+        st = launch_gemm_skinny<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
+    else if (sk2.use)
         st = launch_gemm_splitk<EPI_F16>(w.hq, W2t, T, d_model, d_ff, sk2, w.part, p2, s);
     else
         st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
     if (st != INT8K_OK) return st;
-    const int tn2 = (d_model + BN - 1) / BN;
+    const int tn2 = epi_tiles(T, d_model, d_ff);
     const float* tmax = nullptr;
     if (per_tensor_out) {
         tensor_absmax_kernel<<<1, 256, 0, s>>>(w.p2, (size_t)tn2 * T, w.tmax);

@@ -91,9 +91,15 @@ def test_mlp_bias_vs_oracle(ext, gpu):
     _compare_mlp(_np(out).reshape(T, dm), _np(osc), ref, rsc, "bias")
 
 
-@pytest.mark.parametrize("T,dm,dff", [(128, 1024, 4096), (64, 512, 2048)])
+# Small GEMMs (M N K <= 2^31, K % 512 == 0) take the skinny path (32 x 32 tiles, K split
+# over the waves of a block): 1, 33 (a partial row tile), 64, 128, 200, 256, 300 rows.
+# K not a multiple of 512 takes split-K (128 x 128 tiles, K split over blocks, int32
+# partials): GEMM2 of (96, 512, 1408), both GEMMs of (128, 640, 1408).
+@pytest.mark.parametrize("T,dm,dff", [(128, 1024, 4096), (64, 512, 2048), (1, 512, 1024),
+                                      (33, 512, 1024), (200, 1024, 4096), (256, 512, 2048),
+                                      (300, 512, 1024), (96, 512, 1408), (128, 640, 1408)])
 def test_mlp_few_tokens_split_k(capi_mlp, gpu, T, dm, dff):
-    # decode-time token counts: both GEMMs run split-K (fewer 256 x 256 tiles than CUs)
+    # decode-time token counts: fewer 256 x 256 tiles than CUs
     c, n = _mlp_case(T, dm, dff, seed=T + 5, gpu=gpu)
     out, osc = capi.mlp_forward(c["x"].reshape(T, dm), c["W1"], c["W2"], c["sx"], c["sW1"],
                                 c["sW2"])
@@ -111,6 +117,20 @@ def test_mlp_few_tokens_split_k(capi_mlp, gpu, T, dm, dff):
     ref_t, rsc_t = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], _np(sx1), _np(sw1),
                                  _np(sw2), per_token_out=False, gemm=oracle_c.gemm_i8_i32)
     _compare_mlp(_np(out_t), _np(osc_t), ref_t, rsc_t, f"split-K per-tensor T{T}")
+
+
+@pytest.mark.parametrize("T", [16, 128])
+def test_mlp_few_tokens_bias(ext, gpu, T):
+    # the bias on the skinny path (added before GELU)
+    dm, dff = 512, 2048
+    c, n = _mlp_case(T, dm, dff, seed=T + 77, gpu=gpu)
+    bias = torch.randn(dff, generator=torch.Generator().manual_seed(T)) * 0.5
+    out, osc = ext.int8_mlp_forward_per_channel_bias(c["x"], c["W1"], c["W2"], c["sx"],
+                                                     c["sW1"], c["sW2"], bias.to(gpu))
+    torch.cuda.synchronize()
+    ref, rsc = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                             n["sW2"], bias1=bias.numpy(), gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out).reshape(T, dm), _np(osc), ref, rsc, f"bias T{T}")
 
 
 def test_mlp_per_tensor_reference_config(ext, gpu):
