@@ -532,6 +532,28 @@ def bench_prefill(args):
         ops = 2 * B * H * D * S * (S + 1) if causal else 4 * B * H * S * S * D
         log(f"[bench] prefill causal={causal}: {res_ms[causal] * 1e3:.1f} us  "
             f"{ops / (res_ms[causal] * 1e-3) / 1e12:.1f} TOPS")
+    # the attention output emitted as per-token int8 (fused) against the fp16 output
+    # followed by a separate per-token quantization pass
+    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
+    s8 = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    lib = capi.load()
+    P = capi._ptr
+
+    def fused():
+        capi.check("int8k_attention_forward_quant", lib.int8k_attention_forward_quant(
+            P(c["Qi"]), P(c["Ki"]), P(c["Vi"]), P(q8), P(s8), P(c["sQ"]), P(c["sK"]), P(c["sV"]),
+            B, H, S, D, 1, capi._stream(q8)))
+
+    def two_pass():
+        capi.attention_forward(c["Qi"], c["Ki"], c["Vi"], c["sQ"], c["sK"], c["sV"],
+                               causal=True, out=out)
+        capi.check("int8k_quantize_per_token", lib.int8k_quantize_per_token(
+            P(out), capi.DTYPE_F16, P(q8), P(s8), B * H * S, D, capi._stream(out)))
+
+    ms_fused = time_steps(fused, args.steps, args.warmup, stream)
+    ms_two = time_steps(two_pass, args.steps, args.warmup, stream)
+    log(f"[bench] prefill causal, int8 output: fused {ms_fused * 1e3:.1f} us, "
+        f"fp16 + quantize_per_token {ms_two * 1e3:.1f} us")
     ms = res_ms[True]
     ops = 2 * B * H * D * S * (S + 1)
     tops = ops / (ms * 1e-3) / 1e12
@@ -543,6 +565,8 @@ def bench_prefill(args):
         "data": "synthetic (seeded N(0,1), per-token int8)",
         "config": {"workload": "int8 causal prefill attention B=4 H=32 S=4096 D=128",
                    "noncausal_ms_per_step": round(res_ms[False], 5),
+                   "int8_output_fused_ms_per_step": round(ms_fused, 5),
+                   "int8_output_two_pass_ms_per_step": round(ms_two, 5),
                    "blended_peak_TOPS": round(BLENDED_PEAK, 1)},
         "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
