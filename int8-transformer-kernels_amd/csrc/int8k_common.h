@@ -10,6 +10,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <atomic>
+
 #include "int8k.h"
 
 namespace int8k {
@@ -41,6 +43,27 @@ inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 constexpr size_t kWorkspaceAlign = 256;
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Set-up done once per device: hipFuncSetAttribute (the > 64 KiB dynamic LDS
+// limit) applies to the current device, so a process driving several GPUs
+// configures each.  Devices 0..63 are tracked (others run the set-up on every
+// call); two threads racing on a device only repeat the idempotent set-up, and
+// a failed set-up is tried again on the next call.
+class PerDeviceOnce {
+    std::atomic<uint64_t> done_{0};
+
+public:
+    template <typename F>
+    int run(F&& setup) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return setup();
+        const uint64_t bit = 1ull << dev;
+        if (done_.load(std::memory_order_acquire) & bit) return INT8K_OK;
+        const int st = setup();
+        if (st == INT8K_OK) done_.fetch_or(bit, std::memory_order_release);
+        return st;
+    }
+};
 
 // -------------------------------------------------------------- device side
 

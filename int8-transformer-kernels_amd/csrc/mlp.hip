@@ -783,24 +783,24 @@ MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
     return w;
 }
 
-bool lds_configured = false;
+PerDeviceOnce lds_once;
 
 int configure_lds() {
-    if (lds_configured) return INT8K_OK;
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_I32>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_GELU_F16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
-    if (e != hipSuccess) {
-        set_last_error("hipFuncSetAttribute", e);
-        return INT8K_ERR_HIP;
-    }
-    lds_configured = true;
-    return INT8K_OK;
+    return lds_once.run([] {
+        hipError_t e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_I32>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_GELU_F16>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
+        if (e != hipSuccess) {
+            set_last_error("hipFuncSetAttribute", e);
+            return (int)INT8K_ERR_HIP;
+        }
+        return (int)INT8K_OK;
+    });
 }
 
 }  // namespace

@@ -469,8 +469,8 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
     const long long blocks = (long long)BH * n_qtiles;
     const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
     const int lds = 2 * Stage<D>::kBytes;
-    static bool configured = false;  // > 64 KiB of LDS needs the attribute
-    if (!configured) {
+    static PerDeviceOnce lds_once;  // > 64 KiB of LDS needs the attribute
+    const int st = lds_once.run([lds] {
         hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<D, true>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e == hipSuccess)
@@ -478,10 +478,11 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) {
             set_last_error("hipFuncSetAttribute", e);
-            return INT8K_ERR_HIP;
+            return (int)INT8K_ERR_HIP;
         }
-        configured = true;
-    }
+        return (int)INT8K_OK;
+    });
+    if (st != INT8K_OK) return st;
     if (causal)
         prefill_kernel<D, true><<<(unsigned)blocks, kThreads, lds, stream>>>(
             Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk);
