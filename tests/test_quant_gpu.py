@@ -234,3 +234,25 @@ def test_dequantize_int8_to_fp16_rounds_through_fp32(ext, gpu):
     y = ext.dequantize_int8_to_fp16(torch.from_numpy(codes).to(gpu), float(s))
     np.testing.assert_array_equal(y.cpu().numpy(), O.dequantize_int8_to_fp16(codes, s))
     np.testing.assert_array_equal(y.cpu().numpy(), twice)
+
+
+@pytest.mark.parametrize("cols", [128, 1024, 33])
+def test_quantize_per_token_infinite_element(ext, gpu, cols):
+    # a row with an infinite element has scale inf: its finite elements quantize to 0
+    # (x / inf) and the infinite one to -128 (inf / inf is NaN, and the clamp
+    # max(NaN, -128) gives -128), on the chunked kernels (128, 1024 columns) and the
+    # one-element-per-lane kernel (33 columns); the other rows are unaffected
+    x = torch.randn(4, cols, generator=torch.Generator().manual_seed(cols)).half()
+    x[1, 5] = float("inf")
+    x[2, 0] = float("-inf")
+    q, s = ext.quantize_per_token(x.to(gpu))
+    torch.cuda.synchronize()
+    q, s = q.cpu(), s.cpu()
+    for r, c in ((1, 5), (2, 0)):
+        assert s[r] == float("inf")
+        expect = torch.zeros(cols, dtype=torch.int8)
+        expect[c] = -128
+        assert torch.equal(q[r], expect)
+    rq, rs = O.quantize_per_token(x[[0, 3]].float().numpy())
+    np.testing.assert_array_equal(q[[0, 3]].numpy(), rq)
+    np.testing.assert_array_equal(s[[0, 3]].numpy(), rs)
