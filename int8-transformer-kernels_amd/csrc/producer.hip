@@ -198,15 +198,15 @@ __global__ __launch_bounds__(256) void layernorm_quant_vec_kernel(
     auto add = [](float a, float b) { return a + b; };
     const uint32_t nw = gridDim.x * 4;
     for (uint32_t rb = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; rb < rows; rb += nw * rpw) {
-        const uint32_t r = rb + (lane >> lg);
-        const bool ok = r < rows;
-        const uint32_t rl = min(r, rows - 1);  // loads stay outside divergent branches
+        // rows past the end take the last row and store it again (the same bytes
+        // its own lane stores): no divergent branch around loads or stores
+        const uint32_t r = min(rb + (lane >> lg), rows - 1);
         uint4 w[NCMAX];
         float sum = 0.f;
 #pragma unroll
         for (int i = 0; i < NCMAX; ++i) {
             if (NC > 0 || i < nc) {
-                w[i] = src[(size_t)rl * cpr + ((uint32_t)i << lg) + c0];
+                w[i] = src[(size_t)r * cpr + ((uint32_t)i << lg) + c0];
                 float v[W];
                 unpack_chunk<DT>(w[i], v);
 #pragma unroll
@@ -259,7 +259,6 @@ __global__ __launch_bounds__(256) void layernorm_quant_vec_kernel(
         }
         const float sc = fmaxf(row_reduce(m, lg, [](float a, float b) { return fmaxf(a, b); }),
                                1e-8f) / 127.f;
-        if (!ok) continue;
         const float inv = 1.f / sc;
 #pragma unroll
         for (int i = 0; i < NCMAX; ++i) {
@@ -300,8 +299,9 @@ __global__ __launch_bounds__(256) void quant_heads_vec_kernel(
         uint32_t drow[U], pp[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            // rows past the end load the last row (no divergent branch around the
-            // loads, so they all stay in flight) and are not stored
+            // rows past the end take the last row: they load, quantize and store
+            // it again, the same bytes its own lane stores.  No divergent branch
+            // around the loads or the stores, which keeps them all in flight.
             const uint32_t k = min(kb + u * stride + (lane >> lg), rows - 1);
             pp[u] = k / part_rows;
             drow[u] = k - pp[u] * part_rows;  // (b H + h) S + s
@@ -318,7 +318,6 @@ __global__ __launch_bounds__(256) void quant_heads_vec_kernel(
 #pragma unroll
             for (int e = 0; e < W; ++e) m = fmaxf(m, fabsf(v[e]));
             m = row_reduce(m, lg, [](float a, float b) { return fmaxf(a, b); });
-            if (kb + u * stride + (lane >> lg) >= rows) continue;
             const float sc = fmaxf(m, 1e-8f) / 127.f;
             const float inv = 1.f / sc;
             int8_t* q = pp[u] == 0 ? q0 : (pp[u] == 1 ? q1 : q2);

@@ -154,8 +154,9 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restr
         uint4 w[U][SLOTS];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            // rows past the end load the last row (no divergent branch around the
-            // loads, so they all stay in flight) and are not stored
+            // rows past the end take the last row: they load, quantize and store
+            // it again, the same bytes its own lane stores.  No divergent branch
+            // around the loads or the stores, which keeps them all in flight.
             const uint32_t r = min(rb + u * stride + (lane >> lg), rows - 1);
 #pragma unroll
             for (int i = 0; i < SLOTS; ++i)
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restr
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t r = rb + u * stride + (lane >> lg);
+            const uint32_t r = min(rb + u * stride + (lane >> lg), rows - 1);
             float m = 0.f;
 #pragma unroll
             for (int i = 0; i < SLOTS; ++i) {
@@ -179,20 +180,18 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restr
             const float inv = 1.f / s;
 #pragma unroll
             for (int i = 0; i < SLOTS; ++i) reload_barrier(w[u][i]);
-            if (r < rows) {
-                int8_t* qrow;
-                float* sp;
-                dst(r, qrow, sp);
+            int8_t* qrow;
+            float* sp;
+            dst(r, qrow, sp);
 #pragma unroll
-                for (int i = 0; i < SLOTS; ++i) {
-                    if (NC > 0 || i < nc) {
-                        float v[W];
-                        unpack_chunk<DT>(w[u][i], v);
-                        store_codes<W>(v, s, inv, qrow + (size_t)(((uint32_t)i << lg) + c0) * W);
-                    }
+            for (int i = 0; i < SLOTS; ++i) {
+                if (NC > 0 || i < nc) {
+                    float v[W];
+                    unpack_chunk<DT>(w[u][i], v);
+                    store_codes<W>(v, s, inv, qrow + (size_t)(((uint32_t)i << lg) + c0) * W);
                 }
-                if (c0 == 0) *sp = s;
             }
+            if (c0 == 0) *sp = s;
         }
     }
 }
