@@ -40,9 +40,18 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int kQ = 128;        // queries per block
-constexpr int kKV = 64;        // keys per tile
-constexpr int kThreads = 256;  // 4 waves
+constexpr int kKV = 64;  // keys per tile
+// Block shape per head_dim: one wave per 32 queries.  D = 128 runs 8 waves
+// (256 queries) at 2 waves per SIMD, so each staged K/V tile serves 256
+// queries; D = 64 keeps 4 waves (a 64-key tile has only 256 K chunks of 16 B)
+// and D = 256 keeps 4 waves at one wave per SIMD for its register budget.
+template <int D>
+struct Shape {
+    static constexpr int kWaves = D == 128 ? 8 : 4;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kQ = 32 * kWaves;  // queries per block
+    static constexpr int kMinBlocks = D == 128 ? 1 : (D < 128 ? 2 : 1);
+};
 constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
 // How far (log2 units) a tile's max may exceed the running reference max before
 // O is rescaled: p <= 2^4 on the fast path, so p * sV stays finite in fp16 for
@@ -75,8 +84,10 @@ struct Stage {
     static constexpr int kKBytes = kKV * kKStride;
     static constexpr int kVtBytes = D * kVtStride * 2;
     static constexpr int kBytes = kKBytes + kVtBytes + 2 * kKV * 4;
-    static constexpr int kKChunks = kKV * D / 16 / kThreads;       // 16-B K chunks per thread
-    static constexpr int kVItems = kKV * D / 16 / kThreads;        // 4x4 V blocks per thread
+    static constexpr int kKChunks = kKV * D / 16 / Shape<D>::kThreads;  // 16-B K chunks per thread
+    static constexpr int kVItems = kKV * D / 16 / Shape<D>::kThreads;   // 4x4 V blocks per thread
+    static_assert(kKChunks >= 1 && kKChunks * 16 * Shape<D>::kThreads == kKV * D, "K tile split");
+    static_assert(kVItems >= 1 && kVItems * 16 * Shape<D>::kThreads == kKV * D, "V tile split");
 };
 
 // Buffer resources over one (b,h)'s K, V and scales.  Rows at or past S read
@@ -170,7 +181,7 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
-        const int c = t + n * kThreads;
+        const int c = t + n * Shape<D>::kThreads;
         const int row = c / (D / 16), col = (c % (D / 16)) * 16;
         *reinterpret_cast<int4*>(st + row * Stage<D>::kKStride + col) = pf.k[n];
     }
@@ -179,7 +190,7 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
     constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;
 #pragma unroll
     for (int n = 0; n < Stage<D>::kVItems; ++n) {
-        const int it = t + n * kThreads;
+        const int it = t + n * Shape<D>::kThreads;
         const int kg = v_key_group(it), dg = v_dim_group(it);
         const int p0 = vt_pos(4 * kg);
         const uint2* w = pf.v[n];
@@ -202,7 +213,7 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
+__global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void prefill_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
     const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
     uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qout_scale, int S,
@@ -220,6 +231,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void prefill_kernel(
     const int BH = gridDim.x / n_qtiles;
     const int bh = CAUSAL ? (int)(blockIdx.x % BH) : (int)(blockIdx.x / n_qtiles);
     const int qt = CAUSAL ? n_qtiles - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x % n_qtiles);
+    constexpr int kQ = Shape<D>::kQ;
     const int qw0 = qt * kQ + wave * 32;  // first query of this wave
     const int q = qw0 + (lane & 31);      // this lane's query
     const bool qok = q < S;
@@ -465,6 +477,7 @@ template <int D>
 int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
                    int8_t* qout, float* qscale, const float* sQ, const float* sK, const float* sV,
                    int BH, int S, bool causal, hipStream_t stream) {
+    constexpr int kQ = Shape<D>::kQ, kThreads = Shape<D>::kThreads;
     const int n_qtiles = (S + kQ - 1) / kQ;
     const long long blocks = (long long)BH * n_qtiles;
     const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
@@ -501,7 +514,8 @@ int prefill_entry(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
     const long long BH = (long long)batch * heads;
-    if (BH * ((seq_len + kQ - 1) / kQ) * kThreads >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
+    // work-items of the launch: every Shape has 2 threads per query
+    if (BH * ((seq_len + 127) / 128) * 256 >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
     if ((long long)seq_len * head_dim >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;  // buffer range
     if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) ||
         !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
