@@ -50,7 +50,7 @@ struct Shape {
     static constexpr int kWaves = D == 128 ? 8 : 4;
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kQ = 32 * kWaves;  // queries per block
-    static constexpr int kMinBlocks = D == 128 ? 1 : (D < 128 ? 2 : 1);
+    static constexpr int kMinBlocks = D == 64 ? 2 : 1;  // 2 waves per SIMD at D <= 128
 };
 constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
 // How far (log2 units) a tile's max may exceed the running reference max before
