@@ -484,6 +484,8 @@ torch::Tensor dequantize_per_token_torch(torch::Tensor q, torch::Tensor s,
         TORCH_CHECK(r.sizes() == q.sizes(), "residual must have q's shape");
         TORCH_CHECK(r.device() == q.device(), "residual must be on q's device");
         out_t = r.scalar_type();
+        TORCH_CHECK(!dtype.has_value() || *dtype == out_t,
+                    "dtype must match the residual's dtype, which sets the output dtype");
     } else if (dtype.has_value()) {
         out_t = *dtype;
     }

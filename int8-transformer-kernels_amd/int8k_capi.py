@@ -321,6 +321,8 @@ def dequantize_per_token(q, scales, residual=None, dtype=None):
     cols = q.shape[-1]
     rows = q.numel() // cols
     if residual is not None:
+        if dtype is not None and dtype != residual.dtype:
+            raise ValueError("dtype must match the residual's dtype, which sets the output dtype")
         dtype = residual.dtype
     elif dtype is None:
         dtype = torch.float16

@@ -50,8 +50,8 @@ def test_prefill_reference_configs(ext, gpu, B, H, S, D):
     assert_attn_close(out, _oracle(case, False), f"B{B} H{H} S{S} D{D}")
 
 
-@pytest.mark.parametrize("S,D", [(1, 64), (31, 128), (100, 64), (257, 128), (1000, 256),
-                                 (1024, 128)])
+@pytest.mark.parametrize("S,D", [(1, 64), (31, 128), (100, 64), (200, 128), (257, 128),
+                                 (513, 128), (767, 128), (1000, 256), (1024, 128)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_prefill_ragged_and_causal(ext, gpu, S, D, causal):
     case = workloads.prefill_case(1, 3, S, D, seed=S + D, device=gpu, gen_device="cpu")

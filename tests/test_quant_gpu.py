@@ -186,6 +186,20 @@ def test_dequantize_per_token_capi_unaligned(gpu):
     assert torch.equal(out, (q.float() * s[:, None]).half())
 
 
+def test_dequantize_per_token_dtype_must_match_residual(ext, gpu):
+    # the residual sets the output dtype; a different explicit dtype is an error
+    q = torch.zeros((4, 64), dtype=torch.int8, device=gpu)
+    s = torch.ones(4, dtype=torch.float32, device=gpu)
+    r = torch.zeros((4, 64), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="residual's dtype"):
+        ext.dequantize_per_token(q, s, r, torch.float16)
+    with pytest.raises(ValueError, match="residual's dtype"):
+        capi.dequantize_per_token(q, s, residual=r, dtype=torch.float16)
+    y = ext.dequantize_per_token(q, s, r, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and torch.equal(y, r)
+
+
 def _fp16_double_rounding_cases(rng, count):
     """(q, s) pairs with half(fp32(q * s)) != half(q * s): the fp32 product lands on
     an fp16 tie that the exact product does not.  The dequantizers must give the
