@@ -693,12 +693,15 @@ def bench_block(args):
             qkv = F.layer_norm(x, (self.d,)) @ self.Wqkv
             if int8:
                 qi, sq, ki, sk, vi, sv = ext.quantize_heads(qkv, self.H)
-                a = ext.int8_attention_forward(qi, ki, vi, sq, sk, sv)
+                # rows come out as [B, S, H, Dh], the projection's order: no transpose copy
+                a = ext.int8_attention_forward(qi, ki, vi, sq, sk, sv, out_bshd=True)
+                a = a.view(B, S, self.d)
             else:
                 q, k, v = (t.view(B, S, self.H, self.Dh).transpose(1, 2).contiguous()
                            for t in qkv.split(self.d, dim=-1))
                 a = F.scaled_dot_product_attention(q, k, v)
-            h = x + a.transpose(1, 2).contiguous().view(B, S, self.d) @ self.Wo
+                a = a.transpose(1, 2).contiguous().view(B, S, self.d)
+            h = x + a @ self.Wo
             return self.mlp_int8_residual(h) if int8 else h + self.mlp_fp16(h)
 
         def decode(self, x, kv, int8):

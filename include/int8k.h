@@ -160,11 +160,21 @@ int int8k_decode_attention_forward_paged_quant(
 /*   causal: key j visible to query i iff j <= i.                            */
 /* head_dim must be 64, 128 or 256; seq_len >= 1.  Q, K, V 16-byte aligned,   */
 /* out 8-byte aligned.                                                       */
+/*                                                                          */
+/* flags: INT8K_ATTN_CAUSAL (1) = the causal mask (0 reproduces the          */
+/* reference); INT8K_ATTN_OUT_BSHD (2) = out in [batch, seq_len, heads,      */
+/* head_dim] order, the row order the output projection reads, so no         */
+/* transpose copy is needed between them (the reference block makes one in  */
+/* PyTorch, bench/bench_block.py:121-124).  Other bits are an invalid        */
+/* argument.                                                                 */
 /* ------------------------------------------------------------------------ */
+#define INT8K_ATTN_CAUSAL 1
+#define INT8K_ATTN_OUT_BSHD 2
+
 int int8k_attention_forward(
     const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
     const float* scale_Q, const float* scale_K, const float* scale_V,
-    int batch, int heads, int seq_len, int head_dim, int causal, void* stream);
+    int batch, int heads, int seq_len, int head_dim, int flags, void* stream);
 
 /* Attention output emitted as the next INT8 stage's input: out_q int8
  * [batch, heads, seq_len, head_dim] and out_scale fp32 [batch*heads*seq_len],
@@ -173,11 +183,13 @@ int int8k_attention_forward(
  * through memory.  The attention-output producer fusion the reference names
  * as its next lever (OPTIMIZATION.md:241-246; its callers quantize in
  * PyTorch, bench/bench_block.py:59-63); no counterpart in its kernels.
- * out_q and out_scale 4-byte aligned; otherwise as int8k_attention_forward. */
+ * out_q and out_scale 4-byte aligned; otherwise as int8k_attention_forward,
+ * flags included (with INT8K_ATTN_OUT_BSHD, out_q is [batch, seq_len, heads,
+ * head_dim] and out_scale [batch*seq_len*heads] in that order). */
 int int8k_attention_forward_quant(
     const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* out_q, float* out_scale,
     const float* scale_Q, const float* scale_K, const float* scale_V,
-    int batch, int heads, int seq_len, int head_dim, int causal, void* stream);
+    int batch, int heads, int seq_len, int head_dim, int flags, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* INT8 MLP: Linear -> GELU(tanh) -> Linear with dynamic per-token requant.  */

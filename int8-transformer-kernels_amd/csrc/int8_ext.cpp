@@ -58,11 +58,13 @@ torch::Tensor aligned_i8(const torch::Tensor& t) {
 // with batch*heads*seq_len elements; returns fp16 of Q's shape.  `is_causal`
 // is a new optional trailing argument (default false = the reference's math).
 // With `quant` the output is the per-token int8 of those fp16 rows: {int8 of
-// Q's shape, fp32 scales (batch, heads, seq_len)}.
+// Q's shape, fp32 scales (batch, heads, seq_len)}.  With `out_bshd` the rows
+// come out in (batch, seq_len, heads, ...) order instead, the layout the
+// output projection reads.
 static std::vector<torch::Tensor> attention_impl(torch::Tensor Q, torch::Tensor K,
                                                  torch::Tensor V, torch::Tensor scale_Q,
                                                  torch::Tensor scale_K, torch::Tensor scale_V,
-                                                 bool is_causal, bool quant) {
+                                                 bool is_causal, bool out_bshd, bool quant) {
     TORCH_CHECK(Q.device().is_cuda(), "Q must be a CUDA tensor");
     TORCH_CHECK(Q.dtype() == torch::kInt8, "Q must be int8");
     TORCH_CHECK(K.dtype() == torch::kInt8, "K must be int8");
@@ -91,40 +93,44 @@ static std::vector<torch::Tensor> attention_impl(torch::Tensor Q, torch::Tensor 
     auto sV = scale_V.contiguous().view({n_tokens});
     auto q = aligned_i8(Q), k = aligned_i8(K), v = aligned_i8(V);
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(Q.device());
+    const int flags = (is_causal ? INT8K_ATTN_CAUSAL : 0) | (out_bshd ? INT8K_ATTN_OUT_BSHD : 0);
+    const std::vector<int64_t> rows = out_bshd ? std::vector<int64_t>{batch, seq_len, heads}
+                                               : std::vector<int64_t>{batch, heads, seq_len};
+    std::vector<int64_t> shape = rows;
+    shape.push_back(head_dim);
     if (quant) {
-        auto oq = torch::empty({batch, heads, seq_len, head_dim},
-                               torch::TensorOptions().dtype(torch::kInt8).device(Q.device()));
-        auto os = torch::empty({batch, heads, seq_len},
+        auto oq = torch::empty(shape, torch::TensorOptions().dtype(torch::kInt8).device(Q.device()));
+        auto os = torch::empty(rows,
                                torch::TensorOptions().dtype(torch::kFloat32).device(Q.device()));
         check_status(int8k_attention_forward_quant(
                          q.data_ptr<int8_t>(), k.data_ptr<int8_t>(), v.data_ptr<int8_t>(),
                          oq.data_ptr<int8_t>(), os.data_ptr<float>(), sQ.data_ptr<float>(),
                          sK.data_ptr<float>(), sV.data_ptr<float>(), (int)batch, (int)heads,
-                         (int)seq_len, (int)head_dim, is_causal ? 1 : 0, current_stream(Q)),
+                         (int)seq_len, (int)head_dim, flags, current_stream(Q)),
                      "int8_attention_forward_quant");
         return {oq, os};
     }
-    auto out = torch::empty({batch, heads, seq_len, head_dim},
-                            torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
+    auto out =
+        torch::empty(shape, torch::TensorOptions().dtype(torch::kFloat16).device(Q.device()));
     const int st = int8k_attention_forward(
         q.data_ptr<int8_t>(), k.data_ptr<int8_t>(), v.data_ptr<int8_t>(),
         reinterpret_cast<uint16_t*>(out.data_ptr<at::Half>()), sQ.data_ptr<float>(),
         sK.data_ptr<float>(), sV.data_ptr<float>(), (int)batch, (int)heads, (int)seq_len,
-        (int)head_dim, is_causal ? 1 : 0, current_stream(Q));
+        (int)head_dim, flags, current_stream(Q));
     check_status(st, "int8_attention_forward");
     return {out};
 }
 
 torch::Tensor int8_attention_forward_torch(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                                            torch::Tensor scale_Q, torch::Tensor scale_K,
-                                           torch::Tensor scale_V, bool is_causal) {
-    return attention_impl(Q, K, V, scale_Q, scale_K, scale_V, is_causal, false)[0];
+                                           torch::Tensor scale_V, bool is_causal, bool out_bshd) {
+    return attention_impl(Q, K, V, scale_Q, scale_K, scale_V, is_causal, out_bshd, false)[0];
 }
 
 std::tuple<torch::Tensor, torch::Tensor> int8_attention_forward_quant_torch(
     torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor scale_Q,
-    torch::Tensor scale_K, torch::Tensor scale_V, bool is_causal) {
-    auto r = attention_impl(Q, K, V, scale_Q, scale_K, scale_V, is_causal, true);
+    torch::Tensor scale_K, torch::Tensor scale_V, bool is_causal, bool out_bshd) {
+    auto r = attention_impl(Q, K, V, scale_Q, scale_K, scale_V, is_causal, out_bshd, true);
     return {r[0], r[1]};
 }
 
@@ -752,9 +758,10 @@ std::tuple<torch::Tensor, torch::Tensor> int8_decode_attention_forward_paged_qua
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("int8_attention_forward", &int8_attention_forward_torch,
-          "INT8 attention with per-token quantization — returns FP16 (optional is_causal)",
+          "INT8 attention with per-token quantization — returns FP16 (optional is_causal; "
+          "out_bshd: output as (batch, seq_len, heads, head_dim))",
           py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("scale_Q"), py::arg("scale_K"),
-          py::arg("scale_V"), py::arg("is_causal") = false);
+          py::arg("scale_V"), py::arg("is_causal") = false, py::arg("out_bshd") = false);
     m.def("int8_decode_attention_forward", &int8_decode_attention_forward_torch,
           "INT8 flash-decoding attention (seq_q==1, INT8 KV cache) — returns FP16");
     // Two overloads: scalar scales (per-tensor) and tensor scales (per-token
@@ -805,7 +812,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("int8_attention_forward_quant", &int8_attention_forward_quant_torch,
           "INT8 attention emitting per-token int8 — returns (int8, fp32 scales)",
           py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("scale_Q"), py::arg("scale_K"),
-          py::arg("scale_V"), py::arg("is_causal") = false);
+          py::arg("scale_V"), py::arg("is_causal") = false, py::arg("out_bshd") = false);
     m.def("int8_decode_attention_forward_quant", &int8_decode_attention_forward_quant_torch,
           "INT8 decode attention emitting per-token int8 — returns (int8, fp32 scales)");
     m.def("int8_decode_attention_forward_cache_quant",

@@ -217,7 +217,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
     const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
     uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qout_scale, int S,
-    int n_qtiles, float qk_scale_log2) {
+    int n_qtiles, float qk_scale_log2, int heads, int bshd) {
     constexpr int NS = D / 32;  // 32-wide d slices (QK k-steps) and O^T row tiles
     using St = Stage<D>;
     extern __shared__ __align__(16) char smem[];
@@ -433,6 +433,10 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const float L = sum_xor32(lsum);
     if (!qok) return;  // lanes l and l^32 share q, so both leave or both stay
     const float inv = 1.f / L;
+    // output row: [B, H, S, D] order, or [B, S, H, D] (the row order of the
+    // output projection's input) with bshd
+    const size_t orow_index =
+        bshd ? ((size_t)(bh / heads) * S + q) * heads + (size_t)(bh % heads) : base + q;
     // fp16 output values (rounded from the fp32 quotient); lane l holds
     // d = 32 t + 8 g + 4 h + c of its query, lane l^32 the other half
 #pragma unroll
@@ -448,7 +452,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
         am = max_xor32(am);
         const float sc = fmaxf(am, 1e-8f) / 127.f;
         const float rinv = 1.f / sc;
-        int8_t* qrow = qout + (base + q) * D;
+        int8_t* qrow = qout + orow_index * D;
 #pragma unroll
         for (int t = 0; t < NS; ++t)
 #pragma unroll
@@ -456,10 +460,10 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                 const float y[4] = {o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]};
                 store_codes<4>(y, sc, rinv, qrow + 32 * t + 8 * g + 4 * h);
             }
-        if (h == 0) qout_scale[base + q] = sc;
+        if (h == 0) qout_scale[orow_index] = sc;
         return;
     }
-    uint16_t* orow = out + (base + q) * D;
+    uint16_t* orow = out + orow_index * D;
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
@@ -476,7 +480,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
 template <int D>
 int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
                    int8_t* qout, float* qscale, const float* sQ, const float* sK, const float* sV,
-                   int BH, int S, bool causal, hipStream_t stream) {
+                   int BH, int heads, int S, bool causal, bool bshd, hipStream_t stream) {
     constexpr int kQ = Shape<D>::kQ, kThreads = Shape<D>::kThreads;
     const int n_qtiles = (S + kQ - 1) / kQ;
     const long long blocks = (long long)BH * n_qtiles;
@@ -498,10 +502,10 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
     if (st != INT8K_OK) return st;
     if (causal)
         prefill_kernel<D, true><<<(unsigned)blocks, kThreads, lds, stream>>>(
-            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk);
+            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk, heads, bshd ? 1 : 0);
     else
         prefill_kernel<D, false><<<(unsigned)blocks, kThreads, lds, stream>>>(
-            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk);
+            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk, heads, bshd ? 1 : 0);
     return check_launch("prefill_kernel");
 }
 
@@ -509,8 +513,9 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
 // (fp16) and qout/qscale (int8 + per-token scale) is set.
 int prefill_entry(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out, int8_t* qout,
                   float* qscale, const float* scale_Q, const float* scale_K, const float* scale_V,
-                  int batch, int heads, int seq_len, int head_dim, int causal, void* stream) {
+                  int batch, int heads, int seq_len, int head_dim, int flags, void* stream) {
     if (!Q || !K || !V || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
+    if (flags & ~(INT8K_ATTN_CAUSAL | INT8K_ATTN_OUT_BSHD)) return INT8K_ERR_INVALID_ARGUMENT;
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
     const long long BH = (long long)batch * heads;
@@ -523,17 +528,17 @@ int prefill_entry(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
     if (out ? !aligned_to(out, 8) : !(aligned_to(qout, 4) && aligned_to(qscale, 4)))
         return INT8K_ERR_MISALIGNED;
     hipStream_t s = as_stream(stream);
-    const bool c = causal != 0;
+    const bool c = (flags & INT8K_ATTN_CAUSAL) != 0, bshd = (flags & INT8K_ATTN_OUT_BSHD) != 0;
     switch (head_dim) {
         case 64:
             return launch_prefill<64>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
-                                      (int)BH, seq_len, c, s);
+                                      (int)BH, heads, seq_len, c, bshd, s);
         case 128:
             return launch_prefill<128>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
-                                       (int)BH, seq_len, c, s);
+                                       (int)BH, heads, seq_len, c, bshd, s);
         default:
             return launch_prefill<256>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
-                                       (int)BH, seq_len, c, s);
+                                       (int)BH, heads, seq_len, c, bshd, s);
     }
 }
 
@@ -545,21 +550,21 @@ using namespace int8k;
 extern "C" int int8k_attention_forward(const int8_t* Q, const int8_t* K, const int8_t* V,
                                        uint16_t* out, const float* scale_Q, const float* scale_K,
                                        const float* scale_V, int batch, int heads, int seq_len,
-                                       int head_dim, int causal, void* stream) {
+                                       int head_dim, int flags, void* stream) {
     clear_last_error();
     if (!out) return INT8K_ERR_INVALID_ARGUMENT;
     return prefill_entry(Q, K, V, out, nullptr, nullptr, scale_Q, scale_K, scale_V, batch, heads,
-                         seq_len, head_dim, causal, stream);
+                         seq_len, head_dim, flags, stream);
 }
 
 extern "C" int int8k_attention_forward_quant(const int8_t* Q, const int8_t* K, const int8_t* V,
                                              int8_t* out_q, float* out_scale,
                                              const float* scale_Q, const float* scale_K,
                                              const float* scale_V, int batch, int heads,
-                                             int seq_len, int head_dim, int causal,
+                                             int seq_len, int head_dim, int flags,
                                              void* stream) {
     clear_last_error();
     if (!out_q || !out_scale) return INT8K_ERR_INVALID_ARGUMENT;
     return prefill_entry(Q, K, V, nullptr, out_q, out_scale, scale_Q, scale_K, scale_V, batch,
-                         heads, seq_len, head_dim, causal, stream);
+                         heads, seq_len, head_dim, flags, stream);
 }

@@ -229,16 +229,26 @@ def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, flags=0, out=None, out_scal
 # --------------------------------------------------------------------------
 
 
-def attention_forward(Qi, Ki, Vi, sQ, sK, sV, causal=False, out=None):
-    """Q/K/V int8 [B,H,S,D] (device), per-token fp32 scales (B*H*S) -> fp16 [B,H,S,D]."""
+ATTN_CAUSAL = 1    # INT8K_ATTN_CAUSAL
+ATTN_OUT_BSHD = 2  # INT8K_ATTN_OUT_BSHD
+
+
+def _attn_flags(causal, out_bshd):
+    return (ATTN_CAUSAL if causal else 0) | (ATTN_OUT_BSHD if out_bshd else 0)
+
+
+def attention_forward(Qi, Ki, Vi, sQ, sK, sV, causal=False, out=None, out_bshd=False):
+    """Q/K/V int8 [B,H,S,D] (device), per-token fp32 scales (B*H*S) -> fp16 [B,H,S,D]
+    ([B,S,H,D] with out_bshd)."""
     import torch
 
     B, H, S, D = Qi.shape
     if out is None:
-        out = torch.empty((B, H, S, D), dtype=torch.float16, device=Qi.device)
+        shape = (B, S, H, D) if out_bshd else (B, H, S, D)
+        out = torch.empty(shape, dtype=torch.float16, device=Qi.device)
     st = load().int8k_attention_forward(_ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(out), _ptr(sQ),
-                                        _ptr(sK), _ptr(sV), B, H, S, D, int(bool(causal)),
-                                        _stream(Qi))
+                                        _ptr(sK), _ptr(sV), B, H, S, D,
+                                        _attn_flags(causal, out_bshd), _stream(Qi))
     check("int8k_attention_forward", st)
     return out
 
@@ -253,14 +263,14 @@ def _quant_rows(shape, device):
             torch.empty(shape[:-1], dtype=torch.float32, device=device), n)
 
 
-def attention_forward_quant(Qi, Ki, Vi, sQ, sK, sV, causal=False):
+def attention_forward_quant(Qi, Ki, Vi, sQ, sK, sV, causal=False, out_bshd=False):
     """As attention_forward, emitting the per-token int8 of the fp16 output:
-    (int8 [B,H,S,D], fp32 scales [B,H,S])."""
+    (int8 [B,H,S,D], fp32 scales [B,H,S]), or [B,S,H,D] / [B,S,H] with out_bshd."""
     B, H, S, D = Qi.shape
-    q, s, _ = _quant_rows((B, H, S, D), Qi.device)
+    q, s, _ = _quant_rows((B, S, H, D) if out_bshd else (B, H, S, D), Qi.device)
     st = load().int8k_attention_forward_quant(_ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(q), _ptr(s),
                                               _ptr(sQ), _ptr(sK), _ptr(sV), B, H, S, D,
-                                              int(bool(causal)), _stream(Qi))
+                                              _attn_flags(causal, out_bshd), _stream(Qi))
     check("int8k_attention_forward_quant", st)
     return q, s
 

@@ -59,6 +59,27 @@ def test_prefill_quant_equals_quantized_fp16(ext, gpu, D, S, causal):
     assert np.abs(deq - ref).max() <= 2e-2 + 0.5 * float(s.max())
 
 
+@pytest.mark.parametrize("D,S,causal", [(64, 300, False), (128, 513, True), (256, 77, False)])
+def test_prefill_bshd_output_is_the_transpose(ext, gpu, D, S, causal):
+    # [B, S, H, D] rows (the output projection's order) are the [B, H, S, D] rows,
+    # byte for byte, for the fp16 and the int8 outputs
+    B, H = 2, 3
+    c = workloads.prefill_case(B, H, S, D, seed=7 * D + S, device=gpu)
+    args = (c["Qi"], c["Ki"], c["Vi"], c["sQ"], c["sK"], c["sV"])
+    ref = ext.int8_attention_forward(*args, is_causal=causal)
+    got = ext.int8_attention_forward(*args, is_causal=causal, out_bshd=True)
+    rq, rs = ext.int8_attention_forward_quant(*args, is_causal=causal)
+    q, s = ext.int8_attention_forward_quant(*args, is_causal=causal, out_bshd=True)
+    got2 = capi.attention_forward(*args, causal=causal, out_bshd=True)
+    q2, s2 = capi.attention_forward_quant(*args, causal=causal, out_bshd=True)
+    torch.cuda.synchronize()
+    assert got.shape == (B, S, H, D) and q.shape == (B, S, H, D) and s.shape == (B, S, H)
+    want = ref.transpose(1, 2)
+    assert torch.equal(got, want) and torch.equal(got2, want)
+    _assert_same(q, s, rq.transpose(1, 2), rs.transpose(1, 2), f"bshd D{D} S{S}")
+    _assert_same(q2, s2, rq.transpose(1, 2), rs.transpose(1, 2), "bshd C ABI")
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("nsplit", [0, 1, 5])
 def test_decode_quant_equals_quantized_fp16(ext, gpu, D, nsplit):

@@ -137,6 +137,15 @@ def test_quantized_attention_output_validation(capi):
     assert pre(s=0) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert pre(s=0x48002) == capi.INT8K_ERR_MISALIGNED
     assert pre(D=96) == capi.INT8K_ERR_UNSUPPORTED
+    # flags: bit 0 causal, bit 1 [B,S,H,D] output; any other bit is refused
+    fwd = lambda flags: lib.int8k_attention_forward(  # noqa: E731
+        F(0x10000), F(0x20000), F(0x30000), F(0x40000), F(0x50000), F(0x60000), F(0x70000),
+        1, 2, 64, 96, flags, None)
+    assert capi.ATTN_CAUSAL == 1 and capi.ATTN_OUT_BSHD == 2
+    for flags in (0, 1, 2, 3):  # valid flags reach the head_dim check
+        assert fwd(flags) == capi.INT8K_ERR_UNSUPPORTED
+    for flags in (4, 8, -1):
+        assert fwd(flags) == capi.INT8K_ERR_INVALID_ARGUMENT
     dec = lambda q=0x40000, s=0x48000, ws_bytes=1 << 30: (  # noqa: E731
         lib.int8k_decode_attention_forward_quant(
             F(0x10000), F(0x20000), F(0x30000), F(q), F(s), F(0x50000), F(0x60000), F(0x70000),
