@@ -569,7 +569,8 @@ def bench_prefill(args):
                    "blended_peak_TOPS": round(BLENDED_PEAK, 1)},
         "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
-                     "frac_of_blended_i8_f16": round(tops / BLENDED_PEAK, 4), "traffic": None,
+                     "frac_of_blended_i8_f16": round(tops / BLENDED_PEAK, 4),
+                     "traffic": measured_traffic("prefill_b4h32s4096d128"),
                      "kernel": "prefill_kernel<128, causal>"},
     }
     if not args.no_cpu_baseline:

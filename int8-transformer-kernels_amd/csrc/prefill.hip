@@ -226,11 +226,23 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int wave = threadIdx.x >> 6;
     const int h = lane >> 5;
     // Under the causal mask a query tile's work grows with its index, so the
-    // grid is query-tile-major, heaviest tiles of every (b,h) first; without
-    // it, the query tiles of one (b,h) are adjacent (they share K/V in L2).
+    // grid is query-tile-major, heaviest tiles of every (b,h) first.  Without
+    // it, the query tiles of one (b,h) share its K/V, so they run on one XCD
+    // (one L2): blocks are dispatched to the 8 XCDs in turn, and XCD x takes a
+    // contiguous range of (b,h, query tile) pairs in (b,h)-major order.
     const int BH = gridDim.x / n_qtiles;
-    const int bh = CAUSAL ? (int)(blockIdx.x % BH) : (int)(blockIdx.x / n_qtiles);
-    const int qt = CAUSAL ? n_qtiles - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x % n_qtiles);
+    int bh, qt;
+    if constexpr (CAUSAL) {
+        bh = (int)(blockIdx.x % BH);
+        qt = n_qtiles - 1 - (int)(blockIdx.x / BH);
+    } else {
+        constexpr int kXcds = 8;
+        const int xcd = (int)(blockIdx.x % kXcds), local = (int)(blockIdx.x / kXcds);
+        const int per = (int)(gridDim.x / kXcds), rem = (int)(gridDim.x % kXcds);
+        const int tile = xcd * per + min(xcd, rem) + local;
+        bh = tile / n_qtiles;
+        qt = tile - bh * n_qtiles;
+    }
     constexpr int kQ = Shape<D>::kQ;
     const int qw0 = qt * kQ + wave * 32;  // first query of this wave
     const int q = qw0 + (lane & 31);      // this lane's query
