@@ -393,6 +393,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
     const float* pa = part_acc + (size_t)bh * nsplit * D + lane * DPL;
+    // unrolled so the partial rows of several splits are loaded together (they
+    // come from other XCDs' writes, a full memory round trip each)
+#pragma unroll 8
     for (int s = 0; s < nsplit; ++s) {
         const float w = fast_exp2(ml[2 * s] - M_use);
 #pragma unroll
