@@ -158,8 +158,10 @@ int int8k_decode_attention_forward_paged_quant(
 /*   out fp16 [batch, heads, seq_len, head_dim]                              */
 /*   s_ij = (q_i.k_j) sQ_i sK_j / sqrt(D);  out_i = sum_j softmax_j(s) v_j sV_j*/
 /*   causal: key j visible to query i iff j <= i.                            */
-/* head_dim must be 64, 128 or 256; seq_len >= 1.  Q, K, V 16-byte aligned,   */
-/* out 8-byte aligned.                                                       */
+/* head_dim 1..512; seq_len >= 1.  Multiples of 16 up to 256 run the MFMA   */
+/* kernel (Q, K, V 16-byte aligned, out 8-byte aligned); other head dims run */
+/* a generic kernel (no alignment beyond the element size), as the          */
+/* reference's scalar fallback does (kernels/int8_attention.cu:65-157).      */
 /*                                                                          */
 /* flags: INT8K_ATTN_CAUSAL (1) = the causal mask (0 reproduces the          */
 /* reference); INT8K_ATTN_OUT_BSHD (2) = out in [batch, seq_len, heads,      */

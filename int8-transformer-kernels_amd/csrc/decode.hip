@@ -428,8 +428,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 // NSLOT-aligned and page_size is a multiple of NSLOT, so they sit in one
 // page: one table lookup per group per iteration, then the same immediate
 // slot offsets as the contiguous kernel.  Page p of head h holds
-// K/V [p][h][page_size][D] and scales [p][h][page_size].
-template <int D, int NS, bool FINAL>
+// K/V [p][h][page_size][D] and scales [p][h][page_size].  FL: the
+// non-temporal load flags of the contiguous kernel's tuning for this D.
+template <int D, int NS, bool FINAL, int FL>
 __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ Kp,
     const int8_t* __restrict__ Vp, const float* __restrict__ sQ,
@@ -474,13 +475,13 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
         Int4 kv[NS], vv[NS];
         float sk[NS], sv[NS];
 #pragma unroll
-        for (int t = 0; t < NS; ++t) kv[t] = load_kv16<true>(kp + t * D);
+        for (int t = 0; t < NS; ++t) kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * D);
 #pragma unroll
-        for (int t = 0; t < NS; ++t) vv[t] = load_kv16<true>(vp + t * D);
+        for (int t = 0; t < NS; ++t) vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * D);
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
-            sk[t] = sKp[r0 + t];
-            sv[t] = sVp[r0 + t];
+            sk[t] = load_f32<(FL & kNtScales) != 0>(sKp + r0 + t);
+            sv[t] = load_f32<(FL & kNtScales) != 0>(sVp + r0 + t);
         }
         decode_math<D, NS, false>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
     }
@@ -492,10 +493,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
             const size_t r = row_off(min(row0 + t, j1 - 1));
-            kv[t] = load_kv16<true>(Kp + r * D + sub * 16);
-            vv[t] = load_kv16<true>(Vp + r * D + sub * 16);
-            sk[t] = sKp[r];
-            sv[t] = sVp[r];
+            kv[t] = load_kv16<(FL & kNtKV) != 0>(Kp + r * D + sub * 16);
+            vv[t] = load_kv16<(FL & kNtKV) != 0>(Vp + r * D + sub * 16);
+            sk[t] = load_f32<(FL & kNtScales) != 0>(sKp + r);
+            sv[t] = load_f32<(FL & kNtScales) != 0>(sVp + r);
         }
         decode_math<D, NS, true>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
     }
@@ -600,14 +601,24 @@ int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, con
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
     constexpr int NS = D == 128 ? 8 : 4;
     const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
-    if (final_pass)
-        decode_paged_kernel<D, NS, true><<<grid, kBlockThreads, 0, stream>>>(
-            Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,
-            log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk);
-    else
-        decode_paged_kernel<D, NS, false><<<grid, kBlockThreads, 0, stream>>>(
-            Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,
-            log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk);
+#define INT8K_PAGED_LAUNCH(FIN, FLV)                                                         \
+    decode_paged_kernel<D, NS, FIN, FLV><<<grid, kBlockThreads, 0, stream>>>(                \
+        Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,     \
+        log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk)
+#define INT8K_PAGED_FLAGS(FIN)                          \
+    switch (tuning_for(D).flags & 3) {                  \
+        case 0: INT8K_PAGED_LAUNCH(FIN, 0); break;      \
+        case 1: INT8K_PAGED_LAUNCH(FIN, 1); break;      \
+        case 2: INT8K_PAGED_LAUNCH(FIN, 2); break;      \
+        default: INT8K_PAGED_LAUNCH(FIN, 3); break;     \
+    }
+    if (final_pass) {
+        INT8K_PAGED_FLAGS(true)
+    } else {
+        INT8K_PAGED_FLAGS(false)
+    }
+#undef INT8K_PAGED_FLAGS
+#undef INT8K_PAGED_LAUNCH
     int st = check_launch("decode_paged_kernel");
     if (st != INT8K_OK || final_pass) return st;
     const dim3 gridc((unsigned)ceil_div(BH, kWavesPerBlock));

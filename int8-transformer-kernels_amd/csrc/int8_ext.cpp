@@ -84,8 +84,8 @@ static std::vector<torch::Tensor> attention_impl(torch::Tensor Q, torch::Tensor 
                 "all inputs must be on Q's device");
     const int64_t batch = Q.size(0), heads = Q.size(1), seq_len = Q.size(2),
                   head_dim = Q.size(3);
-    TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256,
-                "prefill attention supports head_dim 64, 128 or 256");
+    TORCH_CHECK(head_dim >= 1 && head_dim <= 512,
+                "prefill attention supports head_dim 1..512");
     TORCH_CHECK(seq_len >= 1 && batch * heads * seq_len <= INT32_MAX, "seq_len out of range");
     const int64_t n_tokens = batch * heads * seq_len;
     auto sQ = scale_Q.contiguous().view({n_tokens});

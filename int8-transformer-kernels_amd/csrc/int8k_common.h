@@ -20,6 +20,8 @@ namespace int8k {
 
 // Records the text of a failing HIP call for int8k_last_error().
 void set_last_error(const char* what, hipError_t err);
+// Records a message of this library's own for int8k_last_error().
+void set_last_error_text(const char* text);
 void clear_last_error();
 
 // Checks the launch that was just enqueued on this thread.

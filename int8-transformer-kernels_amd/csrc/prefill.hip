@@ -8,11 +8,15 @@
 // Non-causal by default (the reference has no mask); `causal` adds the
 // standard lower-triangular mask (key j visible to query i iff j <= i).
 //
-// Design (CDNA4): a block owns 128 queries of one (b,h), 4 waves x 32 queries,
-// and walks the KV sequence in tiles of 64 keys.  Everything is computed
-// transposed so that each lane owns one query:
-//   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows read
-//                                   straight from global/L1, B = Q kept in VGPRs)
+// Design (CDNA4): a block owns the queries of one (b,h), 32 per wave (256
+// queries on 8 waves at head_dim 128, 128 queries on 4 waves at 64 and 256),
+// and walks the KV sequence in tiles of 64 keys.  K (int8 rows), V (as fp16
+// V^T) and both key-scale vectors of a tile are staged in double-buffered LDS
+// by buffer loads: the next tile's loads are in flight in registers while the
+// current tile is computed, and there is one barrier per tile.  Everything is
+// computed transposed so that each lane owns one query:
+//   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows
+//                                   from LDS, B = Q kept in VGPRs)
 //   O^T[D x 32 q]      += V^T . P^T on v_mfma_f32_32x32x16_f16
 // In the 32x32 accumulator layout lane l holds column l%32 — its query — and
 // 16 of the 32 keys, so the row max, the exponentials, the running sum and the
@@ -21,6 +25,12 @@
 // registers it was computed in; V is staged once per tile into LDS as fp16 V^T
 // with the key order permuted to match those P^T registers, so each V^T
 // fragment is a single 16-byte LDS read.
+//
+// Head dims: 64, 128 and 256 run the kernel at their own size; any other
+// multiple of 16 up to 256 runs the next of those sizes with the missing dims
+// read as zero (Q, V) and never stored.  Any other head_dim up to 512 (the
+// reference's scalar fallback, kernels/int8_attention.cu:65-157) runs
+// prefill_generic_kernel.
 //
 // With an int8 destination the epilogue emits the per-token quantization of
 // the fp16 output row instead (the attention output as the next INT8 stage's
@@ -54,9 +64,14 @@ struct Shape {
 };
 constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
 // How far (log2 units) a tile's max may exceed the running reference max before
-// O is rescaled: p <= 2^4 on the fast path, so p * sV stays finite in fp16 for
-// any sV below 4094 (V from fp16 data has sV <= 65504/127 = 516).
+// O is rescaled: p <= 2^4 on the fast path.
 constexpr float kRescaleSlack = 4.0f;
+// P' = fp16(p * sV) is finite for p <= 2^4 only while sV <= 65504 / 2^4.  A
+// tile holding a larger sV (V rows of absmax above ~5.2e5, which fp32 and
+// bf16 sources allow) takes the slow path, where p <= 1 and P' overflows only
+// above sV = 65504, as the reference's P' does (kernels/int8_attention.cu:
+// 530-572).  The tile's flag is set when it is staged.
+constexpr float kFastMaxSv = 65504.0f / 16.0f;
 
 // LDS position of key kk (0..63) of a tile inside a V^T row: keys
 // 16t + 8a + 4h + c are stored at 16t + 8h + 4a + c, so the 8 keys that lane
@@ -77,13 +92,15 @@ __device__ __forceinline__ int v_dim_group(int it) {
     return 4 * (it >> 6) + ((g & 1) << 1 | (g >> 1));
 }
 
-// One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16), scales.
+// One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16), scales,
+// and the tile's large-sV flag (kFastMaxSv).
 template <int D>
 struct Stage {
     static constexpr int kKStride = D + 16;  // bytes per K row
     static constexpr int kKBytes = kKV * kKStride;
     static constexpr int kVtBytes = D * kVtStride * 2;
-    static constexpr int kBytes = kKBytes + kVtBytes + 2 * kKV * 4;
+    static constexpr int kFlagOff = kKBytes + kVtBytes + 2 * kKV * 4;
+    static constexpr int kBytes = kFlagOff + 16;
     static constexpr int kKChunks = kKV * D / 16 / Shape<D>::kThreads;  // 16-B K chunks per thread
     static constexpr int kVItems = kKV * D / 16 / Shape<D>::kThreads;   // 4x4 V blocks per thread
     static_assert(kKChunks >= 1 && kKChunks * 16 * Shape<D>::kThreads == kKV * D, "K tile split");
@@ -92,11 +109,16 @@ struct Stage {
 
 // Buffer resources over one (b,h)'s K, V and scales.  Rows at or past S read
 // as zero, so the tile loads need no clamping; masked keys never reach the
-// output.
+// output.  `dm` is the head_dim of the rows in memory; a padded kernel
+// (dm < D) loads only the K chunks and V dim groups below dm and zeroes the
+// rest (kvalid, vvalid: bit n for item n).
 struct TileSrc {
     __amdgpu_buffer_rsrc_t k, s;
     v4i v;  // V descriptor with a typed format: 8_8_8_8 SSCALED (see load_v_f16x4)
     uint32_t voff_k, voff_v, voff_s;
+    uint32_t kstep, dm;  // bytes between K chunks n and n+1; row stride in memory
+    bool kvalid;
+    uint32_t vvalid;
 };
 
 // A buffer descriptor whose loads convert: data format 8_8_8_8 with numeric
@@ -133,15 +155,25 @@ __device__ __forceinline__ uint2 load_v_f16x4(const v4i& desc, uint32_t voff, ui
 
 template <int D>
 __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t* Vbh,
-                                                 const float* sKbh, const float* sVbh, int S) {
+                                                 const float* sKbh, const float* sVbh, int S,
+                                                 int dm) {
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    constexpr int kT = Shape<D>::kThreads;
     TileSrc src;
-    src.k = make_buffer(Kbh, (uint32_t)S * D);
-    src.v = make_v_descriptor(Vbh, (uint32_t)S * D);
+    src.dm = (uint32_t)dm;
+    src.k = make_buffer(Kbh, (uint32_t)S * dm);
+    src.v = make_v_descriptor(Vbh, (uint32_t)S * dm);
     src.s = make_buffer(wave == 0 ? sKbh : sVbh, (uint32_t)S * 4);  // waves 0 and 1 load scales
-    src.voff_k = (t / (D / 16)) * D + (t % (D / 16)) * 16;
-    src.voff_v = 4 * v_key_group(t) * D + 4 * v_dim_group(t);
+    const int kcol = (t % (D / 16)) * 16;
+    src.voff_k = (t / (D / 16)) * dm + kcol;
+    src.kstep = (uint32_t)(kT * 16 / D) * dm;  // chunk t + n kT is kT*16/D rows further
+    src.kvalid = kcol < dm;
+    src.voff_v = 4 * v_key_group(t) * dm + 4 * v_dim_group(t);
+    src.vvalid = 0;
+#pragma unroll
+    for (int n = 0; n < Stage<D>::kVItems; ++n)
+        if (4 * v_dim_group(t + n * kT) < dm) src.vvalid |= 1u << n;
     src.voff_s = (t & (kKV - 1)) * 4;
     return src;
 }
@@ -154,23 +186,37 @@ struct Prefetch {
     float sc;  // threads 0..63: sK of key tid; 64..127: sV of key tid-64
 };
 
-// Thread t loads 16-byte K chunk t + 256 n (row (t + 256 n) / (D/16); chunks
-// of consecutive n are 4096 bytes apart) and the 4x4 int8 V block t + 256 n
-// (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3; blocks of consecutive n are
-// 16 dim groups = 64 bytes apart).
-template <int D>
+// Thread t (of kT) loads 16-byte K chunk t + kT n (row (t + kT n) / (D/16);
+// chunks of consecutive n are kT*16/D rows apart) and the 4x4 int8 V block
+// t + kT n (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3; blocks of
+// consecutive n are kT/16 dim groups = kT/4 bytes apart).  PAD: chunks and
+// blocks past the memory head_dim are zero.
+template <int D, bool PAD>
 __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& src, int k0) {
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    constexpr int kT = Shape<D>::kThreads;
+    const uint32_t dm = PAD ? src.dm : (uint32_t)D;
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
-        const v4u w = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.voff_k, k0 * D + n * 4096, 0);
-        pf.k[n] = make_int4((int)w.x, (int)w.y, (int)w.z, (int)w.w);
+        if (!PAD || src.kvalid) {
+            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(
+                src.k, src.voff_k, k0 * dm + n * (PAD ? src.kstep : (uint32_t)(kT * 16)), 0);
+            pf.k[n] = make_int4((int)w.x, (int)w.y, (int)w.z, (int)w.w);
+        } else {
+            pf.k[n] = make_int4(0, 0, 0, 0);
+        }
     }
 #pragma unroll
-    for (int n = 0; n < Stage<D>::kVItems; ++n)
+    for (int n = 0; n < Stage<D>::kVItems; ++n) {
+        if (!PAD || (src.vvalid >> n) & 1u) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            pf.v[n][i] = load_v_f16x4(src.v, src.voff_v, k0 * D + n * 64 + i * D);
+            for (int i = 0; i < 4; ++i)
+                pf.v[n][i] = load_v_f16x4(src.v, src.voff_v, k0 * dm + n * (kT / 4) + i * dm);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pf.v[n][i] = make_uint2(0, 0);
+        }
+    }
     if (threadIdx.x < 2 * kKV)
         pf.sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.s, src.voff_s,
                                                                                k0 * 4, 0));
@@ -179,6 +225,11 @@ __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& sr
 template <int D>
 __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
     const int t = threadIdx.x;
+    // wave 1 holds the tile's sV: flag a tile whose P' could overflow on the fast path
+    if (__builtin_amdgcn_readfirstlane(t >> 6) == 1) {
+        const bool big = __ballot(pf.sc > kFastMaxSv) != 0;
+        if (t == 64) *reinterpret_cast<int*>(st + Stage<D>::kFlagOff) = big ? 1 : 0;
+    }
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
         const int c = t + n * Shape<D>::kThreads;
@@ -212,13 +263,16 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
         reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
 }
 
-template <int D, bool CAUSAL>
+// D: the kernel's head_dim.  PAD: the rows in memory have head_dim d_mem < D
+// (a multiple of 16); the dims past it read as zero and are not stored.
+template <int D, bool CAUSAL, bool PAD>
 __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void prefill_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
     const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
     uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qout_scale, int S,
-    int n_qtiles, float qk_scale_log2, int heads, int bshd) {
+    int n_qtiles, float qk_scale_log2, int heads, int bshd, int d_mem) {
     constexpr int NS = D / 32;  // 32-wide d slices (QK k-steps) and O^T row tiles
+    const int dm = PAD ? d_mem : D;  // head_dim of the rows in memory
     using St = Stage<D>;
     extern __shared__ __align__(16) char smem[];
 
@@ -249,9 +303,9 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const bool qok = q < S;
 
     const size_t base = (size_t)bh * S;
-    const int8_t* Qbh = Q + base * D;
-    const int8_t* Kbh = K + base * D;
-    const int8_t* Vbh = V + base * D;
+    const int8_t* Qbh = Q + base * dm;
+    const int8_t* Kbh = K + base * dm;
+    const int8_t* Vbh = V + base * dm;
     const float* sKbh = sK + base;
     const float* sVbh = sV + base;
 
@@ -259,7 +313,9 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     v4i qf[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-        qf[s] = *reinterpret_cast<const v4i*>(Qbh + (size_t)min(q, S - 1) * D + 32 * s + 16 * h);
+        qf[s] = (!PAD || 32 * s + 16 * h < dm)
+                    ? *reinterpret_cast<const v4i*>(Qbh + (size_t)min(q, S - 1) * dm + 32 * s + 16 * h)
+                    : v4i{0, 0, 0, 0};
     const float qscale = qok ? sQ[base + q] * qk_scale_log2 : 0.f;
     const bool qpos = __ballot(!(qscale >= 0.f)) == 0;  // wave-uniform
 
@@ -279,16 +335,16 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     // holds tile kt+1 while tile kt is computed; at the end of the step it is
     // written to the other stage, refilled with tile kt+2, and the step's one
     // barrier follows.
-    const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S);
+    const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
     Prefetch<D> pf;
-    prefetch_tile<D>(pf, src, 0);
+    prefetch_tile<D, PAD>(pf, src, 0);
     commit_tile<D>(pf, smem);
-    if (n_kv > 1) prefetch_tile<D>(pf, src, kKV);
+    if (n_kv > 1) prefetch_tile<D, PAD>(pf, src, kKV);
     __syncthreads();
     auto advance = [&](int kt) {
         if (kt + 1 < n_kv) {
             commit_tile<D>(pf, smem + ((kt + 1) & 1) * St::kBytes);
-            if (kt + 2 < n_kv) prefetch_tile<D>(pf, src, (kt + 2) * kKV);
+            if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pf, src, (kt + 2) * kKV);
         }
         // tile kt+1 is in LDS and every wave is done reading stage kt&1
         __syncthreads();
@@ -326,6 +382,11 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     auto sk_of = [&](int kt) {
         return reinterpret_cast<const float*>(stage_of(kt) + St::kKBytes + St::kVtBytes);
     };
+    // the tile holds an sV above kFastMaxSv (wave-uniform)
+    auto sv_big = [&](int kt) {
+        return __builtin_amdgcn_readfirstlane(
+                   *reinterpret_cast<const int*>(stage_of(kt) + St::kFlagOff)) != 0;
+    };
     // A wave computes tile kt unless the causal mask hides all of it from the wave's queries.
     auto computes = [&](int kt) { return !(CAUSAL && kt * kKV > q_wave_last); };
 
@@ -334,8 +395,8 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     //
     // The running max m is a reference, not necessarily the exact running max: a
     // tile takes the fast path when it has no masked key, every lane's qscale is
-    // >= 0 and no lane's tile max exceeds m by more than kRescaleSlack (log2
-    // units).  Then p = 2^(u*qscale - m) <= 2^kRescaleSlack, O is only updated by
+    // >= 0, no sV of the tile exceeds kFastMaxSv and no lane's tile max exceeds
+    // m by more than kRescaleSlack (log2 units).  Then p = 2^(u*qscale - m) <= 2^kRescaleSlack, O is only updated by
     // the PV MFMAs (in place), and the rescale is skipped.  Every other tile
     // (first tile, masked edge and diagonal tiles, a large max increase) takes the
     // slow path, which sets m to the exact running max and rescales O and l.
@@ -350,7 +411,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                 qk(kt, sacc);
                 const int k0 = kt * kKV;
                 const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
-                if (!(full && qpos)) { slow = true; break; }
+                if (!(full && qpos) || sv_big(kt)) { slow = true; break; }
                 const float* sk_l = sk_of(kt);
                 float u[2][16];
                 float mx = -INFINITY;
@@ -464,23 +525,25 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
         am = max_xor32(am);
         const float sc = fmaxf(am, 1e-8f) / 127.f;
         const float rinv = 1.f / sc;
-        int8_t* qrow = qout + orow_index * D;
+        int8_t* qrow = qout + orow_index * dm;
 #pragma unroll
         for (int t = 0; t < NS; ++t)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
+                const int d = 32 * t + 8 * g + 4 * h;
                 const float y[4] = {o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]};
-                store_codes<4>(y, sc, rinv, qrow + 32 * t + 8 * g + 4 * h);
+                if (!PAD || d < dm) store_codes<4>(y, sc, rinv, qrow + d);
             }
         if (h == 0) qout_scale[orow_index] = sc;
         return;
     }
-    uint16_t* orow = out + orow_index * D;
+    uint16_t* orow = out + orow_index * dm;
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = 32 * t + 8 * g + 4 * h;
+            if (PAD && d >= dm) continue;
             const uint32_t lo = f32_to_f16_bits(o[t][4 * g]) |
                                 ((uint32_t)f32_to_f16_bits(o[t][4 * g + 1]) << 16);
             const uint32_t hi = f32_to_f16_bits(o[t][4 * g + 2]) |
@@ -489,36 +552,244 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
         }
 }
 
-template <int D>
-int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
-                   int8_t* qout, float* qscale, const float* sQ, const float* sK, const float* sV,
-                   int BH, int heads, int S, bool causal, bool bshd, hipStream_t stream) {
-    constexpr int kQ = Shape<D>::kQ, kThreads = Shape<D>::kThreads;
-    const int n_qtiles = (S + kQ - 1) / kQ;
-    const long long blocks = (long long)BH * n_qtiles;
-    const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
-    const int lds = 2 * Stage<D>::kBytes;
-    static PerDeviceOnce lds_once;  // > 64 KiB of LDS needs the attribute
-    const int st = lds_once.run([lds] {
-        hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<D, true>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)prefill_kernel<D, false>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+// ---------------------------------------------------------------- any head_dim
+// Head dims the MFMA kernel does not take (not a multiple of 16, or above 256)
+// up to kGenMaxD, the reference's scalar fallback (kernels/int8_attention.cu:
+// 65-157, 1019-1027) with the same math.  A block holds kGenQ queries of one
+// (b,h), kGenQW per wave, and stages each 64-key tile in LDS: K as zero-padded
+// 4-byte words, V as bytes, the key scales as fp32.  Lane j scores key j of
+// the tile for the wave's queries (v_dot4 over the words: exact int32), the
+// online softmax is a wave reduction, and each lane then accumulates dims
+// d = lane + 64 e over the tile's keys with the weights p_j * sV_j broadcast by
+// v_readlane.  Outputs as prefill_kernel: fp16 rounded from the fp32 quotient,
+// or its per-token int8 codes and scale; [B,H,S,D] or [B,S,H,D] rows.
+constexpr int kGenMaxD = 512;
+constexpr int kGenQW = 4;                // queries per wave
+constexpr int kGenQ = 4 * kGenQW;        // queries per block (4 waves)
+constexpr int kGenKV = 64;               // keys per tile
+constexpr int kGenDims = kGenMaxD / 64;  // dims per lane, at most
+
+// LDS layout of prefill_generic_kernel for head_dim D (bytes).
+struct GenLayout {
+    int dw, ks;  // 4-byte words per row (zero-padded), K row stride in words (odd)
+    int v_off, s_off, q_off, bytes;
+};
+__host__ __device__ inline GenLayout gen_layout(int D) {
+    GenLayout g;
+    g.dw = (D + 3) / 4;
+    g.ks = g.dw | 1;  // odd: the 64 lanes' rows start in 64 different banks
+    g.v_off = kGenKV * g.ks * 4;
+    g.s_off = g.v_off + (kGenKV * D + 15) / 16 * 16;
+    g.q_off = g.s_off + 2 * kGenKV * 4;
+    g.bytes = g.q_off + kGenQ * g.dw * 4;
+    return g;
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void prefill_generic_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const int8_t* __restrict__ V,
+    const float* __restrict__ sQ, const float* __restrict__ sK, const float* __restrict__ sV,
+    uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qout_scale, int S,
+    int D, int n_qtiles, float qk_scale_log2, int heads, int bshd) {
+    extern __shared__ __align__(16) char smem[];
+    const GenLayout L = gen_layout(D);
+    int* kw = reinterpret_cast<int*>(smem);
+    int8_t* vb = reinterpret_cast<int8_t*>(smem + L.v_off);
+    float* ssk = reinterpret_cast<float*>(smem + L.s_off);
+    float* ssv = ssk + kGenKV;
+    int* qw = reinterpret_cast<int*>(smem + L.q_off);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // causal grids: heaviest query tiles of every (b,h) first
+    const int BH = gridDim.x / n_qtiles;
+    int bh, qt;
+    if constexpr (CAUSAL) {
+        bh = (int)(blockIdx.x % BH);
+        qt = n_qtiles - 1 - (int)(blockIdx.x / BH);
+    } else {
+        bh = (int)(blockIdx.x / n_qtiles);
+        qt = (int)(blockIdx.x % n_qtiles);
+    }
+    const int q0 = qt * kGenQ;
+    const size_t base = (size_t)bh * S;
+    const int rowb = L.dw * 4;  // bytes per zero-padded row
+
+    int8_t* qb = reinterpret_cast<int8_t*>(qw);
+    for (int i = t; i < kGenQ * rowb; i += 256) {
+        const int r = i / rowb, c = i - r * rowb;
+        qb[i] = (q0 + r < S && c < D) ? Q[(base + q0 + r) * D + c] : (int8_t)0;
+    }
+    float qs[kGenQW], m[kGenQW], l[kGenQW], acc[kGenQW][kGenDims];
+#pragma unroll
+    for (int i = 0; i < kGenQW; ++i) {
+        const int q = q0 + wave * kGenQW + i;
+        qs[i] = q < S ? sQ[base + q] * qk_scale_log2 : 0.f;
+        m[i] = -INFINITY;
+        l[i] = 0.f;
+#pragma unroll
+        for (int e = 0; e < kGenDims; ++e) acc[i][e] = 0.f;
+    }
+    const int nd = (D + 63) >> 6;
+    const int kv_end = CAUSAL ? min(S, q0 + kGenQ) : S;
+    for (int k0 = 0; k0 < kv_end; k0 += kGenKV) {
+        __syncthreads();  // the previous tile's reads are done
+        int8_t* kb = reinterpret_cast<int8_t*>(kw);
+        const int krow = L.ks * 4;
+        for (int i = t; i < kGenKV * krow; i += 256) {
+            const int r = i / krow, c = i - r * krow;
+            kb[i] = (k0 + r < S && c < D) ? K[(base + k0 + r) * D + c] : (int8_t)0;
+        }
+        const int vn = min(kGenKV, S - k0) * D;
+        for (int i = t; i < kGenKV * D; i += 256) vb[i] = i < vn ? V[(base + k0) * D + i] : (int8_t)0;
+        if (t < kGenKV) ssk[t] = k0 + t < S ? sK[base + k0 + t] : 0.f;
+        else if (t < 2 * kGenKV) ssv[t - kGenKV] = k0 + t - kGenKV < S ? sV[base + k0 + t - kGenKV] : 0.f;
+        __syncthreads();
+
+        const int key = k0 + lane;
+        const float skl = ssk[lane], svl = ssv[lane];
+        const int* kr = kw + lane * L.ks;
+        float w[kGenQW];
+#pragma unroll
+        for (int i = 0; i < kGenQW; ++i) {
+            const int qi = wave * kGenQW + i, q = q0 + qi;
+            const int* qr = qw + qi * L.dw;
+            int dot = 0;
+            for (int c = 0; c < L.dw; ++c) dot = __builtin_amdgcn_sdot4(qr[c], kr[c], dot, false);
+            float s = static_cast<float>(dot) * qs[i] * skl;
+            if (key >= S || (CAUSAL && key > q)) s = -INFINITY;
+            float mx = s;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float m_new = fmaxf(m[i], mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float corr = fast_exp2(m[i] - m_use);
+            const float p = fast_exp2(s - m_use);
+            float ps = p;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) ps += __shfl_xor(ps, off);
+            l[i] = l[i] * corr + ps;
+#pragma unroll
+            for (int e = 0; e < kGenDims; ++e) acc[i][e] *= corr;
+            m[i] = m_new;
+            w[i] = p * svl;
+        }
+        const int nk = min(kGenKV, kv_end - k0);
+        for (int j = 0; j < nk; ++j) {
+            float v[kGenDims];
+#pragma unroll
+            for (int e = 0; e < kGenDims; ++e) {
+                const int d = lane + 64 * e;
+                v[e] = (e < nd && d < D) ? static_cast<float>(vb[j * D + d]) : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < kGenQW; ++i) {
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), j));
+#pragma unroll
+                for (int e = 0; e < kGenDims; ++e) acc[i][e] = fmaf(wj, v[e], acc[i][e]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < kGenQW; ++i) {
+        const int q = q0 + wave * kGenQW + i;
+        if (q >= S) break;  // wave-uniform
+        const float inv = 1.f / l[i];
+        const size_t orow =
+            bshd ? ((size_t)(bh / heads) * S + q) * heads + (size_t)(bh % heads) : base + q;
+        float y[kGenDims];
+#pragma unroll
+        for (int e = 0; e < kGenDims; ++e) y[e] = __half2float(f16_of_f32(acc[i][e] * inv));
+        if (qout != nullptr) {
+            float am = 0.f;
+#pragma unroll
+            for (int e = 0; e < kGenDims; ++e)
+                if (e < nd && lane + 64 * e < D) am = fmaxf(am, fabsf(y[e]));
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+            const float sc = fmaxf(am, 1e-8f) / 127.f;
+#pragma unroll
+            for (int e = 0; e < kGenDims; ++e) {
+                const int d = lane + 64 * e;
+                if (e < nd && d < D) qout[orow * D + d] = (int8_t)quant_code(y[e], sc);
+            }
+            if (lane == 0) qout_scale[orow] = sc;
+        } else {
+#pragma unroll
+            for (int e = 0; e < kGenDims; ++e) {
+                const int d = lane + 64 * e;
+                if (e < nd && d < D) out[orow * D + d] = f32_to_f16_bits(y[e]);
+            }
+        }
+    }
+}
+
+// Dynamic LDS above 64 KiB needs the attribute, once per device and kernel.
+template <typename... Kernels>
+int set_lds_limit(PerDeviceOnce& once, int bytes, Kernels... kernels) {
+    return once.run([=] {
+        hipError_t e = hipSuccess;
+        for (const void* k : {reinterpret_cast<const void*>(kernels)...}) {
+            if (e == hipSuccess)
+                e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        }
         if (e != hipSuccess) {
             set_last_error("hipFuncSetAttribute", e);
             return (int)INT8K_ERR_HIP;
         }
         return (int)INT8K_OK;
     });
+}
+
+// D: the kernel's head_dim; dm: the head_dim of the rows in memory (dm <= D,
+// a multiple of 16; dm < D runs the padded instance).
+template <int D>
+int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+                   int8_t* qout, float* qscale, const float* sQ, const float* sK, const float* sV,
+                   int BH, int heads, int S, int dm, bool causal, bool bshd, hipStream_t stream) {
+    constexpr int kQ = Shape<D>::kQ, kThreads = Shape<D>::kThreads;
+    const int n_qtiles = (S + kQ - 1) / kQ;
+    const long long blocks = (long long)BH * n_qtiles;
+    const float qk = (1.0f / std::sqrt((float)dm)) * kLog2e;
+    const int lds = 2 * Stage<D>::kBytes;
+    static PerDeviceOnce lds_once;
+    const int st = set_lds_limit(lds_once, lds, prefill_kernel<D, true, false>,
+                                 prefill_kernel<D, false, false>, prefill_kernel<D, true, true>,
+                                 prefill_kernel<D, false, true>);
     if (st != INT8K_OK) return st;
-    if (causal)
-        prefill_kernel<D, true><<<(unsigned)blocks, kThreads, lds, stream>>>(
-            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk, heads, bshd ? 1 : 0);
-    else
-        prefill_kernel<D, false><<<(unsigned)blocks, kThreads, lds, stream>>>(
-            Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk, heads, bshd ? 1 : 0);
+    const int b = bshd ? 1 : 0;
+#define INT8K_PREFILL_LAUNCH(C, P)                                                         \
+    prefill_kernel<D, C, P><<<(unsigned)blocks, kThreads, lds, stream>>>(                  \
+        Q, K, V, sQ, sK, sV, out, qout, qscale, S, n_qtiles, qk, heads, b, dm)
+    if (dm == D) {
+        if (causal) INT8K_PREFILL_LAUNCH(true, false);
+        else INT8K_PREFILL_LAUNCH(false, false);
+    } else {
+        if (causal) INT8K_PREFILL_LAUNCH(true, true);
+        else INT8K_PREFILL_LAUNCH(false, true);
+    }
+#undef INT8K_PREFILL_LAUNCH
     return check_launch("prefill_kernel");
+}
+
+int launch_prefill_generic(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+                           int8_t* qout, float* qscale, const float* sQ, const float* sK,
+                           const float* sV, int BH, int heads, int S, int D, bool causal,
+                           bool bshd, hipStream_t stream) {
+    const int n_qtiles = (S + kGenQ - 1) / kGenQ;
+    const long long blocks = (long long)BH * n_qtiles;
+    const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
+    static PerDeviceOnce lds_once;
+    const int st = set_lds_limit(lds_once, gen_layout(kGenMaxD).bytes,
+                                 prefill_generic_kernel<true>, prefill_generic_kernel<false>);
+    if (st != INT8K_OK) return st;
+    const int lds = gen_layout(D).bytes;
+    if (causal)
+        prefill_generic_kernel<true><<<(unsigned)blocks, 256, lds, stream>>>(
+            Q, K, V, sQ, sK, sV, out, qout, qscale, S, D, n_qtiles, qk, heads, bshd ? 1 : 0);
+    else
+        prefill_generic_kernel<false><<<(unsigned)blocks, 256, lds, stream>>>(
+            Q, K, V, sQ, sK, sV, out, qout, qscale, S, D, n_qtiles, qk, heads, bshd ? 1 : 0);
+    return check_launch("prefill_generic_kernel");
 }
 
 // Shared checks and dispatch of both entry points: exactly one of out
@@ -528,30 +799,39 @@ int prefill_entry(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* o
                   int batch, int heads, int seq_len, int head_dim, int flags, void* stream) {
     if (!Q || !K || !V || !scale_Q || !scale_K || !scale_V) return INT8K_ERR_INVALID_ARGUMENT;
     if (flags & ~(INT8K_ATTN_CAUSAL | INT8K_ATTN_OUT_BSHD)) return INT8K_ERR_INVALID_ARGUMENT;
-    if (batch <= 0 || heads <= 0 || seq_len <= 0) return INT8K_ERR_INVALID_ARGUMENT;
-    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return INT8K_ERR_UNSUPPORTED;
+    if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0)
+        return INT8K_ERR_INVALID_ARGUMENT;
+    if (head_dim > kGenMaxD) return INT8K_ERR_UNSUPPORTED;
     const long long BH = (long long)batch * heads;
-    // work-items of the launch: every Shape has 2 threads per query
-    if (BH * ((seq_len + 127) / 128) * 256 >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
+    const bool mfma = head_dim % 16 == 0 && head_dim <= 256;
+    // work-items of the launch: 2 threads per query (MFMA kernel), 16 (generic)
+    if (BH * (((long long)seq_len + 127) / 128) * 256 >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;
+    if (!mfma && BH * (((long long)seq_len + kGenQ - 1) / kGenQ) * 256 >= (1LL << 32))
+        return INT8K_ERR_UNSUPPORTED;
     if ((long long)seq_len * head_dim >= (1LL << 32)) return INT8K_ERR_UNSUPPORTED;  // buffer range
-    if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16) ||
-        !aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
+    if (!aligned_to(scale_Q, 4) || !aligned_to(scale_K, 4) || !aligned_to(scale_V, 4))
         return INT8K_ERR_MISALIGNED;
-    if (out ? !aligned_to(out, 8) : !(aligned_to(qout, 4) && aligned_to(qscale, 4)))
+    if (mfma) {
+        if (!aligned_to(Q, 16) || !aligned_to(K, 16) || !aligned_to(V, 16))
+            return INT8K_ERR_MISALIGNED;
+        if (out ? !aligned_to(out, 8) : !(aligned_to(qout, 4) && aligned_to(qscale, 4)))
+            return INT8K_ERR_MISALIGNED;
+    } else if (out ? !aligned_to(out, 2) : !aligned_to(qscale, 4)) {
         return INT8K_ERR_MISALIGNED;
+    }
     hipStream_t s = as_stream(stream);
     const bool c = (flags & INT8K_ATTN_CAUSAL) != 0, bshd = (flags & INT8K_ATTN_OUT_BSHD) != 0;
-    switch (head_dim) {
-        case 64:
-            return launch_prefill<64>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
-                                      (int)BH, heads, seq_len, c, bshd, s);
-        case 128:
-            return launch_prefill<128>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
-                                       (int)BH, heads, seq_len, c, bshd, s);
-        default:
-            return launch_prefill<256>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
-                                       (int)BH, heads, seq_len, c, bshd, s);
-    }
+    if (!mfma)
+        return launch_prefill_generic(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
+                                      (int)BH, heads, seq_len, head_dim, c, bshd, s);
+    if (head_dim <= 64)
+        return launch_prefill<64>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V, (int)BH,
+                                  heads, seq_len, head_dim, c, bshd, s);
+    if (head_dim <= 128)
+        return launch_prefill<128>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V,
+                                   (int)BH, heads, seq_len, head_dim, c, bshd, s);
+    return launch_prefill<256>(Q, K, V, out, qout, qscale, scale_Q, scale_K, scale_V, (int)BH,
+                               heads, seq_len, head_dim, c, bshd, s);
 }
 
 }  // namespace

@@ -12,6 +12,8 @@ void set_last_error(const char* what, hipError_t err) {
                    hipGetErrorString(err) + ")";
 }
 
+void set_last_error_text(const char* text) { g_last_error = text; }
+
 void clear_last_error() { g_last_error.clear(); }
 
 }  // namespace int8k

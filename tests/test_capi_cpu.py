@@ -75,9 +75,13 @@ def test_prefill_argument_validation(capi):
     assert f(Q=0) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert f(S=0) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert f(B=-1) == capi.INT8K_ERR_INVALID_ARGUMENT
-    assert f(D=96) == capi.INT8K_ERR_UNSUPPORTED
+    assert f(D=0) == capi.INT8K_ERR_INVALID_ARGUMENT
+    assert f(D=513) == capi.INT8K_ERR_UNSUPPORTED
     assert f(Q=0x10008) == capi.INT8K_ERR_MISALIGNED
     assert f(out=0x40002) == capi.INT8K_ERR_MISALIGNED
+    # head dims off the MFMA kernel (generic kernel) need only element alignment
+    assert f(D=96, Q=0x10008) == capi.INT8K_ERR_MISALIGNED  # 96: padded MFMA kernel
+    assert f(D=72, out=0x40001) == capi.INT8K_ERR_MISALIGNED
 
 
 def test_mlp_argument_validation(capi):
@@ -136,11 +140,11 @@ def test_quantized_attention_output_validation(capi):
     assert pre(q=0) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert pre(s=0) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert pre(s=0x48002) == capi.INT8K_ERR_MISALIGNED
-    assert pre(D=96) == capi.INT8K_ERR_UNSUPPORTED
+    assert pre(D=600) == capi.INT8K_ERR_UNSUPPORTED
     # flags: bit 0 causal, bit 1 [B,S,H,D] output; any other bit is refused
     fwd = lambda flags: lib.int8k_attention_forward(  # noqa: E731
         F(0x10000), F(0x20000), F(0x30000), F(0x40000), F(0x50000), F(0x60000), F(0x70000),
-        1, 2, 64, 96, flags, None)
+        1, 2, 64, 600, flags, None)
     assert capi.ATTN_CAUSAL == 1 and capi.ATTN_OUT_BSHD == 2
     for flags in (0, 1, 2, 3):  # valid flags reach the head_dim check
         assert fwd(flags) == capi.INT8K_ERR_UNSUPPORTED

@@ -136,11 +136,14 @@ def test_decode_baseline_cfg1(capi, ext, gpu):
     assert np.abs(ref_np - ref.reshape(12, 64)).max() < 1e-9
 
 
-@pytest.mark.parametrize("B,H,D,S", [(32, 32, 128, 8192), (8, 32, 64, 32768)])
-def test_decode_baseline_full_size_sampled(capi, ext, gpu, B, H, D, S):
-    # BASELINE configs 2 and 3 at full size with 1% outlier channels x8; the
-    # oracle checks a seeded sample of 24 (b,h) rows, the rest is covered by
-    # finiteness and the |out| <= max|V_deq| convexity bound.
+@pytest.mark.parametrize("B,H,D,S", [(32, 32, 128, 8192), (8, 32, 64, 32768),
+                                     (8, 32, 64, 2048), (8, 32, 64, 4096), (8, 32, 64, 8192),
+                                     (8, 32, 64, 16384)])
+def test_decode_baseline_full_size(capi, ext, gpu, B, H, D, S):
+    # BASELINE configs 2 and 3 and config 3's ctx sweep at full size, 1% outlier
+    # channels x8: every (b,h) row against the C oracle, plus finiteness and the
+    # |out| <= max|V_deq| convexity bound.
+    print(f"decode full size B{B} H{H} D{D} S{S}", flush=True)
     case = workloads.decode_case(B, H, D, S, seed=99, outlier_frac=0.01, device=gpu)
     out = ext.int8_decode_attention_forward(case["Qi"], case["Ki"], case["Vi"], case["sQ"],
                                             case["sK"], case["sV"])
@@ -149,9 +152,8 @@ def test_decode_baseline_full_size_sampled(capi, ext, gpu, B, H, D, S):
     assert torch.isfinite(o).all()
     vmax = (case["Vi"].abs().float().amax(dim=-1) * case["sV"]).amax(dim=-1).reshape(B * H)
     assert (o.abs().amax(dim=-1) <= vmax * (1 + 1e-3) + 1e-6).all()
-    rows = np.random.default_rng(0).choice(B * H, size=24, replace=False)
-    ref = _oracle(case, rows=rows)
-    assert_attn_close(o.cpu().numpy()[rows], ref, f"full B{B} H{H} D{D} S{S}")
+    ref = _oracle(case)
+    assert_attn_close(o.cpu().numpy(), ref, f"full B{B} H{H} D{D} S{S}")
 
 
 def test_decode_ext_scale_shapes_and_views(ext, gpu):
