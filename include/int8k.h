@@ -86,6 +86,24 @@ int int8k_decode_attention_forward_quant(
 /* The split count the forward call uses for this shape (after clamping). */
 int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
 
+/* int8k_decode_attention_forward without a workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  It allocates nothing: the split partials go to a device array
+ * the library holds, INT8K_DECODE_NOALLOC_SCRATCH_BYTES per GPU, from the
+ * library's load until the process ends.  A call whose
+ * int8k_decode_attention_workspace_bytes() exceeds that size returns
+ * INT8K_ERR_WORKSPACE (int8k_last_error() says why) before touching the GPU.
+ * All calls on one GPU share its array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.  Same
+ * arguments, results and alignment as int8k_decode_attention_forward. */
+#define INT8K_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+
+int int8k_decode_attention_forward_noalloc(
+    const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* out,
+    const float* scale_Q, const float* scale_K, const float* scale_V,
+    int BH, int S, int head_dim, int nsplit, void* stream);
+
 /* Decode over a preallocated KV cache: K_cache/V_cache int8 [BH, capacity, D],
  * sK_cache/sV_cache fp32 [BH*capacity]; the first S positions of each (b,h)
  * are attended (S <= capacity).  Same math and workspace as

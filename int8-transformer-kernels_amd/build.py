@@ -31,7 +31,8 @@ LIB_NAME = "libint8k.so"
 CALIB_LIB_NAME = "libint8k_calib.so"
 EXT_NAME = "int8_ext"
 
-HIP_SOURCES = ["status.hip", "decode.hip", "mlp.hip", "prefill.hip", "quant.hip", "producer.hip"]
+HIP_SOURCES = ["status.hip", "decode.hip", "mlp.hip", "prefill.hip", "quant.hip", "producer.hip",
+               "noalloc.hip"]
 
 # -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code.
 HIP_FLAGS = [

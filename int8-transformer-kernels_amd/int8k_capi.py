@@ -60,6 +60,7 @@ _SIGNATURES = {
     "int8k_decode_attention_forward_quant": (_I, [_P] * 8 + [_I] * 4 + [_P, _SZ, _P]),
     "int8k_decode_attention_forward_cache_quant": (_I, [_P] * 8 + [_I] * 5 + [_P, _SZ, _P]),
     "int8k_decode_attention_forward_paged_quant": (_I, [_P] * 10 + [_I] * 8 + [_P, _SZ, _P]),
+    "int8k_decode_attention_forward_noalloc": (_I, [_P] * 7 + [_I] * 4 + [_P]),
 }
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
@@ -145,6 +146,18 @@ def decode_attention(Qi, Ki, Vi, sQ, sK, sV, nsplit: int = 0, out=None, workspac
         _ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(out), _ptr(sQ), _ptr(sK), _ptr(sV),
         BH, S, D, nsplit, _ptr(workspace), workspace.numel(), _stream(Qi))
     check("int8k_decode_attention_forward", st)
+    return out
+
+
+def decode_attention_noalloc(Qi, Ki, Vi, sQ, sK, sV, out, nsplit: int = 0):
+    """decode_attention into a caller-given `out` [BH,D] fp16, with the split partials in the
+    library's own scratch (int8k_decode_attention_forward_noalloc): no device allocation."""
+    BH, D = Qi.shape[0], Qi.shape[-1]
+    S = Ki.numel() // (BH * D)
+    st = load().int8k_decode_attention_forward_noalloc(
+        _ptr(Qi), _ptr(Ki), _ptr(Vi), _ptr(out), _ptr(sQ), _ptr(sK), _ptr(sV),
+        BH, S, D, nsplit, _stream(Qi))
+    check("int8k_decode_attention_forward_noalloc", st)
     return out
 
 
