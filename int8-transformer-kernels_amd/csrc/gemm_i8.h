@@ -242,6 +242,167 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
     }
 }
 
+// ------------------------------------------------------------ fp16 A operand
+// The MLP's second GEMM can read the fp16 hidden h [M][K] itself and quantize
+// it per row on its way to LDS: code = rint(clamp(h * inv_row, -128, 127)),
+// inv_row = 127 / amax_row, the codes of the separate requantization pass
+// (requant_rows_kernel) for every finite h.  Each thread's 8 A chunks lie on
+// 8 fixed rows (c / 8 for chunk c), so their inv sit in registers.
+
+// rint(fl(h * inv)) of the 16 fp16 of a chunk as 16 packed int8.  fl(h * inv)
+// is one v_fma_mix_f32 with a +0 addend (one rounding, as the pass's
+// multiply; the sign of a zero product does not reach the code).  Adding
+// 1.5 * 2^23 rounds half to even onto the integer grid and leaves the code in
+// the low byte of the sum's bits for |h * inv| < 2^22; |h| <= amax (1 + 2^-11)
+// keeps |h * inv| below 127.5, so no clamp is needed.  EXACT (a block with a
+// row max above the fp16 range, whose h may be infinite) clamps first, as the
+// pass does.
+template <bool EXACT>
+__device__ __forceinline__ int4 quant_chunk_f16(const uint4 (&h)[2], float inv) {
+#pragma clang fp contract(off)
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t w[8] = {h[0].x, h[0].y, h[0].z, h[0].w, h[1].x, h[1].y, h[1].z, h[1].w};
+    uint32_t t[16];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const h2 v = __builtin_bit_cast(h2, w[j]);
+        float p0 = __builtin_fmaf((float)v.x, inv, 0.0f);
+        float p1 = __builtin_fmaf((float)v.y, inv, 0.0f);
+        if constexpr (EXACT) {
+            p0 = fminf(fmaxf(p0, -128.f), 127.f);
+            p1 = fminf(fmaxf(p1, -128.f), 127.f);
+        }
+        t[2 * j] = __float_as_uint(p0 + 12582912.0f);
+        t[2 * j + 1] = __float_as_uint(p1 + 12582912.0f);
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        o[q] = __builtin_amdgcn_perm(t[4 * q + 1], t[4 * q], 0x0c0c0400u) |
+               __builtin_amdgcn_perm(t[4 * q + 3], t[4 * q + 2], 0x04000c0cu);
+    return make_int4((int)o[0], (int)o[1], (int)o[2], (int)o[3]);
+}
+
+// Chunk i of this thread (16 elements of row (t + 256 i) / 8): the 32 bytes of
+// fp16, clamped in bounds like load_chunk.
+__device__ __forceinline__ void load_chunk_f16(uint4 (&dst)[2], const uint16_t* __restrict__ A16,
+                                               int rows, int K, int ld, int r0, int k0, int i) {
+    const int c = threadIdx.x + i * kThreads;
+    const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+    const int gk = min(k0 + kc, K - 16);
+    const uint4* p = reinterpret_cast<const uint4*>(A16 + (size_t)min(r0 + row, rows - 1) * ld + gk);
+    dst[0] = p[0];
+    dst[1] = p[1];
+}
+
+constexpr int kSchedValu = 0x002;
+
+// mainloop with an fp16 A: the same schedule, plus the conversion of the next
+// stage's A chunks (loaded a whole K-step earlier) threaded between the MFMAs
+// of slices 0 and 1 (chunks 0-3 and 4-7), so slice 2 only stores the codes.
+// inv[i]: the row scale of chunk i's row.
+template <bool EDGE, bool EXACT>
+__device__ __forceinline__ void mainloop_a16(v16i (&acc)[TM][TN], const uint16_t* __restrict__ A16,
+                                             const int8_t* __restrict__ Bt, int M, int N, int K,
+                                             int lda, int ldb, int m0, int n0, char* lds,
+                                             const float (&inv)[kChunks]) {
+    static_assert(BK == 128 && kChunks == 8, "schedule written for 4 k-slices and 8 chunks");
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int nk = (K + BK - 1) / BK;
+    const int a_off = (wm * WM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    const int b_off = A_STAGE + (wn * WN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    uint4 ar[kChunks][2];  // raw fp16 A of the stage after next
+    int4 aq[kChunks];      // codes of the next stage's A
+    int4 br[kChunks];
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        load_chunk_f16(ar[i], A16, M, K, lda, m0, 0, i);
+        br[i] = load_chunk(Bt, N, K, ldb, n0, 0, i);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        store_chunk<EDGE>(quant_chunk_f16<EXACT>(ar[i], inv[i]), lds, M, K, m0, 0, i);
+        store_chunk<EDGE>(br[i], lds + A_STAGE, N, K, n0, 0, i);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        load_chunk_f16(ar[i], A16, M, K, lda, m0, BK, i);
+        br[i] = load_chunk(Bt, N, K, ldb, n0, BK, i);
+    }
+    __syncthreads();
+    v4i a[2][TM], b[2][TN];
+    read_slice(a[0], b[0], lds, a_off, b_off, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const char* cur = lds + (kt & 1) * STAGE_BYTES;
+        char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
+        __builtin_amdgcn_sched_barrier(0);
+        // slice 0: reads of slice 1, conversion of chunks 0-3
+        read_slice(a[1], b[1], cur, a_off, b_off, 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aq[i] = quant_chunk_f16<EXACT>(ar[i], inv[i]);
+        mfma_slice(acc, a[0], b[0]);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            if (g < 8) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 11, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // slice 1: reads of slice 2, conversion of chunks 4-7
+        read_slice(a[0], b[0], cur, a_off, b_off, 2);
+#pragma unroll
+        for (int i = 4; i < 8; ++i) aq[i] = quant_chunk_f16<EXACT>(ar[i], inv[i]);
+        mfma_slice(acc, a[1], b[1]);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            if (g < 8) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 11, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // slice 2: reads of slice 3, the next stage's stores, the loads of the one after
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const int i = g >> 2, j = g & 3;
+            if (g < 4) a[1][g] = read_frag(cur, a_off, g, 3);
+            else if (g < 8) b[1][g - 4] = read_frag(cur, b_off, g - 4, 3);
+            if (g < 8) {
+                store_chunk<EDGE>(aq[g], nxt, M, K, m0, (kt + 1) * BK, g);
+                load_chunk_f16(ar[g], A16, M, K, lda, m0, (kt + 2) * BK, g);
+            } else {
+                store_chunk<EDGE>(br[g - 8], nxt + A_STAGE, N, K, n0, (kt + 1) * BK, g - 8);
+                br[g - 8] = load_chunk(Bt, N, K, ldb, n0, (kt + 2) * BK, g - 8);
+            }
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 8; g < 16; ++g) {
+            if (g < 12) a[0][g - 8] = read_frag(nxt, a_off, g - 8, 0);
+            else b[0][g - 12] = read_frag(nxt, b_off, g - 12, 0);
+            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
 // Accumulator element r of a 32x32 MFMA tile held by `lane`:
 //   row = (r/4)*8 + (lane/32)*4 + r%4,  col = lane%32.
 __device__ __forceinline__ int acc_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }

@@ -18,6 +18,9 @@
 // — no atomics, no zero-fill), requant_rows_kernel (reduces the partials,
 // requantizes a row), tensor_absmax_kernel and transpose_i8_kernel (weight
 // packing to the K-contiguous [N][K] layout the MFMA operands want).
+// gemm_i8_a16_kernel is GEMM2 reading the fp16 hidden and quantizing it per
+// row on load (no requant pass, no int8 hidden in memory); same bytes, slower
+// on MI355X, so it runs only when INT8K_MLP_GEMM2_FP16_HIDDEN=1.
 //
 // Few tokens (decode-time MLPs, T = B): 256 x 256 tiles leave most CUs idle
 // (T = 128 gives 16 blocks for GEMM1 and 4 for GEMM2).  When a GEMM has fewer
@@ -28,6 +31,7 @@
 // partials), so requant_rows_kernel and every result are the same on both
 // paths.
 #include <algorithm>
+#include <cstdlib>
 
 #include "gemm_i8.h"
 
@@ -224,6 +228,38 @@ __device__ __forceinline__ void epilogue_edge(const v16i (&acc)[TM][TN], const E
     }
 }
 
+// The tile's epilogue after the main loop: fp16 stores and the per-(tile, row)
+// absmax partial pmax[tn][row].  pre_sa/pre_sb/pre_b: this thread's row scale
+// (row m0 + t), column scale and bias (column n0 + t), loaded before the main
+// loop so it hides their latency.
+template <int EPI>
+__device__ __forceinline__ void epilogue_tile(const v16i (&acc)[TM][TN], const EpiParams& p, int M,
+                                              int N, int m0, int n0, int tn, float pre_sa,
+                                              float pre_sb, float pre_b, char* lds) {
+    // Row absmax of this block's tile: rowmax[wn][row] from each column
+    // half of the waves, combined below (values >= 0, so integer max on
+    // the bit pattern orders them like floats).  The scale region lies
+    // past the stages; the row maxima reuse stage 0, whose last reads
+    // (operands past the end of K) are never used.
+    int* rowmax = reinterpret_cast<int*>(lds);
+    float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
+    float* esb = esa + BM;
+    float* ebias = esb + BN;
+    esa[threadIdx.x] = pre_sa;
+    esb[threadIdx.x] = pre_sb;
+    ebias[threadIdx.x] = pre_b;
+    __syncthreads();
+    if (m0 + BM <= M && n0 + BN <= N && (size_t)BM * p.ldc * 2 < (1ull << 32))
+        epilogue_interior<EPI>(acc, p, m0, n0, rowmax, esa, esb, ebias);
+    else
+        epilogue_edge<EPI>(acc, p, M, N, m0, n0, rowmax, esa, esb, ebias);
+    __syncthreads();
+    const int row = m0 + threadIdx.x;
+    if (row < M)
+        p.pmax[(size_t)tn * M + row] =
+            __int_as_float(max(rowmax[threadIdx.x], rowmax[BM + threadIdx.x]));
+}
+
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int M, int N, int K, int lda,
@@ -267,29 +303,49 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
             }
         return;
     } else {
-        // Row absmax of this block's tile: rowmax[wn][row] from each column
-        // half of the waves, combined below (values >= 0, so integer max on
-        // the bit pattern orders them like floats).  The scale region lies
-        // past the stages; the row maxima reuse stage 0, whose last reads
-        // (operands past the end of K) are never used.
-        int* rowmax = reinterpret_cast<int*>(lds);
-        float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
-        float* esb = esa + BM;
-        float* ebias = esb + BN;
-        esa[threadIdx.x] = pre_sa;
-        esb[threadIdx.x] = pre_sb;
-        ebias[threadIdx.x] = pre_b;
-        __syncthreads();
-        if (m0 + BM <= M && n0 + BN <= N && (size_t)BM * p.ldc * 2 < (1ull << 32))
-            epilogue_interior<EPI>(acc, p, m0, n0, rowmax, esa, esb, ebias);
-        else
-            epilogue_edge<EPI>(acc, p, M, N, m0, n0, rowmax, esa, esb, ebias);
-        __syncthreads();
-        const int row = m0 + threadIdx.x;
-        if (row < M)
-            p.pmax[(size_t)tn * M + row] =
-                __int_as_float(max(rowmax[threadIdx.x], rowmax[BM + threadIdx.x]));
+        epilogue_tile<EPI>(acc, p, M, N, m0, n0, tn, pre_sa, pre_sb, pre_b, lds);
     }
+}
+
+// The MLP's GEMM2 over the fp16 hidden A16 [M][K] itself, with no
+// requantization pass and no int8 hidden in memory: each block reduces its 256
+// rows' absmax from GEMM1's partials (pmax1, tn1 per row) as
+// requant_rows_kernel does, quantizes A on its way to LDS (mainloop_a16) and
+// runs gemm_i8_kernel<EPI_F16>'s epilogue with the hidden row scale
+// amax / 127.
+constexpr int kA16LdsBytes = kEpiLdsBytes + BM * 4;  // + the rows' 127 / amax
+
+__global__ __launch_bounds__(kThreads, 1) void gemm_i8_a16_kernel(
+    const uint16_t* __restrict__ A16, const int8_t* __restrict__ Bt, int M, int N, int K,
+    int tiles_m, int tiles_n, const float* __restrict__ pmax1, int tn1, EpiParams p) {
+    extern __shared__ __align__(16) char lds[];
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x;
+    const int row = min(m0 + t, M - 1);
+    float mx = 0.f;
+    for (int j = 0; j < tn1; ++j) mx = fmaxf(mx, pmax1[(size_t)j * M + row]);
+    const float amax = fmaxf(mx, 1e-8f);
+    const float pre_sa = amax / 127.f;
+    const float pre_sb = p.sb[(size_t)min(n0 + t, N - 1) * p.sb_stride];
+    float* einv = reinterpret_cast<float*>(lds + kEpiLdsBytes);
+    einv[t] = 127.f / amax;
+    // a row max past the fp16 range: some h may be infinite, so clamp before rounding
+    const bool exact = __syncthreads_or(!(amax <= 65504.f)) != 0;
+    float inv[kChunks];
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) inv[i] = einv[(t + i * kThreads) / kChunksPerRow];
+    v16i acc[TM][TN];
+    const bool interior = m0 + BM <= M && n0 + BN <= N && K % BK == 0;
+    if (exact) {
+        if (interior) mainloop_a16<false, true>(acc, A16, Bt, M, N, K, K, K, m0, n0, lds, inv);
+        else mainloop_a16<true, true>(acc, A16, Bt, M, N, K, K, K, m0, n0, lds, inv);
+    } else {
+        if (interior) mainloop_a16<false, false>(acc, A16, Bt, M, N, K, K, K, m0, n0, lds, inv);
+        else mainloop_a16<true, false>(acc, A16, Bt, M, N, K, K, K, m0, n0, lds, inv);
+    }
+    epilogue_tile<EPI_F16>(acc, p, M, N, m0, n0, tn, pre_sa, pre_sb, 0.f, lds);
 }
 
 // ---------------------------------------------------------------- split-K path
@@ -783,6 +839,17 @@ MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
     return w;
 }
 
+// Whether the tiled GEMM2 reads the fp16 hidden with on-load quantization
+// (gemm_i8_a16_kernel) instead of the int8 hidden of requant_rows_kernel.
+// Both give the same bytes; the default is the separate pass, measured faster
+// on MI355X at the BASELINE shape (the on-load path doubles GEMM2's A bytes
+// and adds ~3 VALU ops per element to a loop that has no VALU slack).
+// INT8K_MLP_GEMM2_FP16_HIDDEN=1 selects the on-load path, read on every call.
+bool gemm2_reads_fp16_hidden() {
+    const char* e = std::getenv("INT8K_MLP_GEMM2_FP16_HIDDEN");
+    return e != nullptr && e[0] == '1';
+}
+
 PerDeviceOnce lds_once;
 
 int configure_lds() {
@@ -795,6 +862,9 @@ int configure_lds() {
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_a16_kernel,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kA16LdsBytes);
         if (e != hipSuccess) {
             set_last_error("hipFuncSetAttribute", e);
             return (int)INT8K_ERR_HIP;
@@ -891,13 +961,8 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     else
         st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     if (st != INT8K_OK) return st;
-    // per-token requant of the hidden (one absmax partial per row and 256-column
-    // tile, or per 32-column block of the skinny path)
-    const int tn1 = epi_tiles(T, d_ff, d_model);
-    if ((st = launch_requant(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T, d_ff, s)) !=
-        INT8K_OK)
-        return st;
     // GEMM2 + dequant epilogue -> fp16 output + absmax partials
+    const int tn1 = epi_tiles(T, d_ff, d_model);
     EpiParams p2{};
     p2.c16 = w.o16;
     p2.ldc = d_model;
@@ -907,13 +972,27 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p2.sb_stride = n_scale_W2 == 1 ? 0 : 1;
     p2.pmax = w.p2;
     const SplitKPlan sk2 = splitk_plan(T, d_model, d_ff);
-    if (use_skinny(T, d_model, d_ff))
-        st = launch_gemm_skinny<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
-    else if (sk2.use)
-        st = launch_gemm_splitk<EPI_F16>(w.hq, W2t, T, d_model, d_ff, sk2, w.part, p2, s);
-    else
-        st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
-    if (st != INT8K_OK) return st;
+    const bool skinny2 = use_skinny(T, d_model, d_ff);
+    if (!skinny2 && !sk2.use && gemm2_reads_fp16_hidden()) {
+        // the tiled GEMM2 reads the fp16 hidden and quantizes it per row on load
+        const int tiles_m = (T + BM - 1) / BM, tiles_n = (d_model + BN - 1) / BN;
+        gemm_i8_a16_kernel<<<tiles_m * tiles_n, kThreads, kA16LdsBytes, s>>>(
+            w.h16, W2t, T, d_model, d_ff, tiles_m, tiles_n, w.p1, tn1, p2);
+        if ((st = check_launch("gemm_i8_a16_kernel")) != INT8K_OK) return st;
+    } else {
+        // per-token requant of the hidden (one absmax partial per row and 256-column
+        // tile, or per 32-column block of the skinny path)
+        if ((st = launch_requant(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T, d_ff,
+                                 s)) != INT8K_OK)
+            return st;
+        if (skinny2)
+            st = launch_gemm_skinny<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
+        else if (sk2.use)
+            st = launch_gemm_splitk<EPI_F16>(w.hq, W2t, T, d_model, d_ff, sk2, w.part, p2, s);
+        else
+            st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
+        if (st != INT8K_OK) return st;
+    }
     const int tn2 = epi_tiles(T, d_model, d_ff);
     const float* tmax = nullptr;
     if (per_tensor_out) {

@@ -204,6 +204,32 @@ def test_mlp_argument_errors(ext, gpu):
                              torch.zeros(128, 60, dtype=torch.int8, device=gpu), 1.0, 1.0, 1.0)
 
 
+@pytest.mark.parametrize("T,dm,dff,big_rows", [(1024, 1024, 4096, False),
+                                                (700, 528, 1040, False),
+                                                (1024, 1024, 4096, True)])
+def test_mlp_gemm2_on_fp16_hidden_matches_requant_pass(capi_mlp, gpu, monkeypatch, T, dm, dff,
+                                                        big_rows):
+    # These shapes run GEMM2 as the 256 x 256 tiled kernel.  With
+    # INT8K_MLP_GEMM2_FP16_HIDDEN=1 it reads the fp16 hidden and quantizes it per row
+    # on load; by default a separate pass writes the int8 hidden.  The codes must be the
+    # same, so the outputs are equal byte for byte.  big_rows: a few token rows scaled
+    # so their hidden exceeds the fp16 range (infinite h, the clamping path).
+    c, n = _mlp_case(T, dm, dff, seed=T + dff, gpu=gpu)
+    if big_rows:
+        c["sx"][::97] *= 2e5
+        n["sx"] = _np(c["sx"])
+    args = (c["x"].reshape(T, dm), c["W1"], c["W2"], c["sx"], c["sW1"], c["sW2"])
+    monkeypatch.delenv("INT8K_MLP_GEMM2_FP16_HIDDEN", raising=False)
+    out_a, osc_a = capi.mlp_forward(*args)
+    monkeypatch.setenv("INT8K_MLP_GEMM2_FP16_HIDDEN", "1")
+    out_b, osc_b = capi.mlp_forward(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b) and torch.equal(osc_a, osc_b)
+    ref, rsc = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                             n["sW2"], gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out_b), _np(osc_b), ref, rsc, f"T{T} dm{dm} dff{dff} big={big_rows}")
+
+
 def test_mlp_baseline_cfg4_full_size(ext, gpu):
     # T=4096, 4096 -> 16384 -> 4096, per-token / per-channel.  Every
     # row against the oracle (its exact int8 GEMMs in C), in blocks of 512 tokens (the
