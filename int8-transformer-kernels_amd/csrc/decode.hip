@@ -71,6 +71,20 @@ struct SplitPlan {
     int chunk;
 };
 
+// Most chunks per (b,h) that run as one launch (decode_block_kernel: one wave
+// per chunk, merged in LDS); larger plans run the split + combine pair.
+constexpr int kMaxBlockSplits = 16;
+
+// Plans of at most kMaxBlockSplits chunks run as one launch (decode_block_kernel);
+// INT8K_DECODE_BLOCK=0 keeps them on the split + combine pair (read once).
+bool use_block_kernel() {
+    static const bool on = [] {
+        const char* e = std::getenv("INT8K_DECODE_BLOCK");
+        return !(e != nullptr && e[0] == '0');
+    }();
+    return on;
+}
+
 inline int env_int(const char* name, int dflt) {
     const char* e = std::getenv(name);
     return e ? std::atoi(e) : dflt;
@@ -109,8 +123,11 @@ SplitPlan plan_splits(int BH, int S, int D, int nsplit_req) {
         ns = nsplit_req;
     } else {
         ns = ceil_div(tn.target_units, BH);
-        // keep at least 4 iterations per unit unless S is short
-        const long long by_len = std::max<long long>(1, ceil_div(S, 4LL * R));
+        // keep at least 4 iterations per unit unless S is short; an under-filled
+        // grid (few (b,h)) may still take up to kMaxBlockSplits one-iteration
+        // chunks, which the one-launch kernel merges on chip
+        const long long by_len = std::max<long long>(
+            1, std::max(ceil_div(S, 4LL * R), std::min<long long>(kMaxBlockSplits, ceil_div(S, R))));
         ns = std::min(ns, by_len);
     }
     ns = std::max<long long>(1, std::min(ns, max_split));
@@ -364,9 +381,38 @@ __global__ __launch_bounds__(kBlockThreads) void decode_split_kernel(
     finish_unit<D, FINAL>(m, l, acc, grp, sub, unit, part_ml, part_acc, out);
 }
 
-// Pass 2: one wave per bh merges its nsplit partial states into the fp16 row,
-// or with qout set into the per-token int8 quantization of that fp16 row
-// (codes and scale as int8k_quantize_per_token gives for it).
+// The output row of one (b,h) from the merged accumulator (dims lane*D/64 ..
+// +D/64 of this lane) and the merged sum L: the fp16 row, or with qout set the
+// per-token int8 quantization of that fp16 row (codes and scale as
+// int8k_quantize_per_token gives for it).  A whole wave calls it.
+template <int D>
+__device__ __forceinline__ void emit_row(const float (&acc)[D / 64], float L, int lane, int bh,
+                                         uint16_t* __restrict__ out, int8_t* __restrict__ qout,
+                                         float* __restrict__ qscale) {
+    constexpr int DPL = D / 64;
+    const float inv = L > 0.f ? 1.f / L : 0.f;  // no rows at all (empty sequence): zeros
+    float y[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) y[i] = __half2float(f16_of_f32(acc[i] * inv));
+    if (qout != nullptr) {
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) am = fmaxf(am, fabsf(y[i]));
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+        const float sc = fmaxf(am, 1e-8f) / 127.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i)
+            qout[(size_t)bh * D + lane * DPL + i] = (int8_t)quant_code(y[i], sc);
+        if (lane == 0) qscale[bh] = sc;
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i)
+        out[(size_t)bh * D + lane * DPL + i] = __half_as_ushort(__float2half_rn(y[i]));
+}
+
+// Pass 2: one wave per bh merges its nsplit partial states into the output row.
 template <int D>
 __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
     const float* __restrict__ part_ml, const float* __restrict__ part_acc,
@@ -401,26 +447,103 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 #pragma unroll
         for (int i = 0; i < DPL; ++i) acc[i] = fmaf(pa[(size_t)s * D + i], w, acc[i]);
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;  // no rows at all (empty sequence): zeros
-    float y[DPL];
+    emit_row<D>(acc, L, lane, bh, out, qout, qscale);
+}
+
+// One launch for plans of at most kMaxBlockSplits chunks per (b,h): block bh
+// runs one wave per chunk (blockDim.x / 64 waves), each wave walks its chunk as
+// the split kernel does, merges its row groups and leaves (m, l, acc[D]) in
+// LDS; wave 0 then merges the chunks with the log-sum-exp rule and writes the
+// row.  No partial state leaves the chip and there is no second launch.
+
+template <int D, int NS, bool VEC_SCALES, int FL>
+__global__ __launch_bounds__(64 * kMaxBlockSplits) void decode_block_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ K,
+    const int8_t* __restrict__ V, const float* __restrict__ sQ,
+    const float* __restrict__ sK, const float* __restrict__ sV, uint16_t* __restrict__ out,
+    int8_t* __restrict__ qout, float* __restrict__ qscale, int S, int S_cap, int chunk,
+    float qk_scale_log2, int stagger) {
+    using G = DecodeGeom<D, NS>;
+    constexpr int LPR = D / 16;
+    __shared__ float s_ml[kMaxBlockSplits][2];
+    __shared__ __align__(16) float s_acc[kMaxBlockSplits][D];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int bh = blockIdx.x;
+    const int j0 = w * chunk;
+    const int j1 = min(S, j0 + chunk);
+    const int sub = lane % LPR;
+    const int grp = lane / LPR;
+
+    const Int4 q = load16(Q + (size_t)bh * D + sub * 16);
+    const float qscale_l = sQ[bh] * qk_scale_log2;
+    const int8_t* Kbh = K + (size_t)bh * S_cap * D;
+    const int8_t* Vbh = V + (size_t)bh * S_cap * D;
+    const float* sKbh = sK + (size_t)bh * S_cap;
+    const float* sVbh = sV + (size_t)bh * S_cap;
+
+    float m = -INFINITY, l = 0.f;
+    float acc[16];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) y[i] = __half2float(f16_of_f32(acc[i] * inv));
-    if (qout != nullptr) {
-        float am = 0.f;
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) am = fmaxf(am, fabsf(y[i]));
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
-        const float sc = fmaxf(am, 1e-8f) / 127.f;
-#pragma unroll
-        for (int i = 0; i < DPL; ++i)
-            qout[(size_t)bh * D + lane * DPL + i] = (int8_t)quant_code(y[i], sc);
-        if (lane == 0) qscale[bh] = sc;
-        return;
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
+    const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
+    int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
+    for (int k = 0; k < n_full; ++k) {
+        decode_iter<D, NS, false, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh,
+                                                  j0 + it * G::kRowsPerIter + grp * NS, j1, sub,
+                                                  q, qscale_l, m, l, acc);
+        it = (it + 1 == n_full) ? 0 : it + 1;
     }
+    const int base = j0 + n_full * G::kRowsPerIter;
+    if (base < j1)
+        decode_iter<D, NS, true, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, base + grp * NS, j1, sub,
+                                                 q, qscale_l, m, l, acc);
+
+    // merge the wave's row groups (lanes with equal `sub`)
+    float M = m;
 #pragma unroll
-    for (int i = 0; i < DPL; ++i)
-        out[(size_t)bh * D + lane * DPL + i] = __half_as_ushort(__float2half_rn(y[i]));
+    for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+    const float f = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
+    float Lw = l * f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= f;
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+        Lw += __shfl_xor(Lw, off);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
+    }
+    if (grp == 0) {
+        float4* dst = reinterpret_cast<float4*>(&s_acc[w][sub * 16]);
+        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+        dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+        if (sub == 0) {
+            s_ml[w][0] = M;
+            s_ml[w][1] = Lw;
+        }
+    }
+    __syncthreads();
+    if (w != 0) return;
+    // wave 0: the log-sum-exp merge of the chunks, as decode_combine_kernel
+    constexpr int DPL = D / 64;
+    float Mall = -INFINITY;
+    for (int c = 0; c < nw; ++c) Mall = fmaxf(Mall, s_ml[c][0]);
+    const float M_use = (Mall == -INFINITY) ? 0.f : Mall;
+    float L = 0.f;
+    float o[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+    for (int c = 0; c < nw; ++c) {
+        const float wt = fast_exp2(s_ml[c][0] - M_use);
+        L += s_ml[c][1] * wt;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] = fmaf(s_acc[c][lane * DPL + i], wt, o[i]);
+    }
+    emit_row<D>(o, L, lane, bh, out, qout, qscale);
 }
 
 // Paged variant of pass 1.  Unit = (b, h, split) as above, over positions
@@ -430,7 +553,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 // slot offsets as the contiguous kernel.  Page p of head h holds
 // K/V [p][h][page_size][D] and scales [p][h][page_size].  FL: the
 // non-temporal load flags of the contiguous kernel's tuning for this D.
-template <int D, int NS, bool FINAL, int FL>
+// VEC_SCALES: a group's NS scales load as 16-byte vectors (its rows are
+// NS-aligned inside one page; needs 16-byte aligned scale arrays).
+template <int D, int NS, bool FINAL, int FL, bool VEC_SCALES>
 __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ Kp,
     const int8_t* __restrict__ Vp, const float* __restrict__ sQ,
@@ -438,7 +563,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
     float* __restrict__ part_ml, float* __restrict__ part_acc, uint16_t* __restrict__ out,
     int H, int num_pages, int log2_page, int max_pages, int nsplit, int chunk, int units,
-    float qk_scale_log2) {
+    float qk_scale_log2, int stagger) {
     using G = DecodeGeom<D, NS>;
     const int lane = threadIdx.x & 63;
     const int unit = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
@@ -467,9 +592,16 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
+    // Iterations start at a unit-dependent rotation (stagger), and the page id of
+    // the next iteration is looked up while the current one computes, so the
+    // table load is not a dependent load in front of every iteration's K/V loads.
+    int it = stagger ? (int)(((unsigned)unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
+    size_t r_next = n_full > 0 ? row_off(j0 + it * G::kRowsPerIter + grp * NS) : 0;
     for (int k = 0; k < n_full; ++k) {
-        const int row0 = j0 + k * G::kRowsPerIter + grp * NS;
-        const size_t r0 = row_off(row0);
+        const int row0 = j0 + it * G::kRowsPerIter + grp * NS;
+        const size_t r0 = r_next;
+        it = (it + 1 == n_full) ? 0 : it + 1;
+        if (k + 1 < n_full) r_next = row_off(j0 + it * G::kRowsPerIter + grp * NS);
         const int8_t* kp = Kp + r0 * D + sub * 16;
         const int8_t* vp = Vp + r0 * D + sub * 16;
         Int4 kv[NS], vv[NS];
@@ -478,10 +610,27 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
         for (int t = 0; t < NS; ++t) kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * D);
 #pragma unroll
         for (int t = 0; t < NS; ++t) vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * D);
+        if constexpr (VEC_SCALES) {
 #pragma unroll
-        for (int t = 0; t < NS; ++t) {
-            sk[t] = load_f32<(FL & kNtScales) != 0>(sKp + r0 + t);
-            sv[t] = load_f32<(FL & kNtScales) != 0>(sVp + r0 + t);
+            for (int t = 0; t < NS; t += 4) {
+                typedef float v4f __attribute__((ext_vector_type(4)));
+                v4f a, b;
+                if constexpr ((FL & kNtScales) != 0) {
+                    a = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sKp + r0 + t));
+                    b = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sVp + r0 + t));
+                } else {
+                    a = *reinterpret_cast<const v4f*>(sKp + r0 + t);
+                    b = *reinterpret_cast<const v4f*>(sVp + r0 + t);
+                }
+                sk[t] = a.x; sk[t + 1] = a.y; sk[t + 2] = a.z; sk[t + 3] = a.w;
+                sv[t] = b.x; sv[t + 1] = b.y; sv[t + 2] = b.z; sv[t + 3] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NS; ++t) {
+                sk[t] = load_f32<(FL & kNtScales) != 0>(sKp + r0 + t);
+                sv[t] = load_f32<(FL & kNtScales) != 0>(sVp + r0 + t);
+            }
         }
         decode_math<D, NS, false>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
     }
@@ -535,6 +684,23 @@ void launch_split(int flags, int stagger, dim3 grid, hipStream_t stream, const i
 #undef INT8K_SPLIT_LAUNCH
 }
 
+template <int D, int NS, bool VEC>
+void launch_block(int flags, int stagger, int BH, hipStream_t stream, const int8_t* Q,
+                  const int8_t* K, const int8_t* V, const float* sQ, const float* sK,
+                  const float* sV, uint16_t* out, int8_t* qout, float* qs, int S, int S_cap,
+                  const SplitPlan& plan, float qk) {
+#define INT8K_BLOCK_LAUNCH(FLV)                                                             \
+    decode_block_kernel<D, NS, VEC, FLV><<<(unsigned)BH, 64 * plan.nsplit, 0, stream>>>(    \
+        Q, K, V, sQ, sK, sV, out, qout, qs, S, S_cap, plan.chunk, qk, stagger)
+    switch (flags & 3) {
+        case 0: INT8K_BLOCK_LAUNCH(0); break;
+        case 1: INT8K_BLOCK_LAUNCH(1); break;
+        case 2: INT8K_BLOCK_LAUNCH(2); break;
+        default: INT8K_BLOCK_LAUNCH(3); break;
+    }
+#undef INT8K_BLOCK_LAUNCH
+}
+
 template <int D, bool VEC, bool FINAL>
 void launch_split_ns(int ns, int flags, int stagger, dim3 grid, hipStream_t stream,
                      const int8_t* Q, const int8_t* K, const int8_t* V, const float* sQ,
@@ -570,6 +736,17 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, const Decod
     const int sg = tn.stagger;
     const int u = (int)units;
     const float qk = qk_scale_log2;
+    if (plan.nsplit <= kMaxBlockSplits && use_block_kernel()) {
+        // one launch: the chunks of a (b,h) are the waves of one block
+        if (ns == 4) {
+            if (vec) launch_block<D, 4, true>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+            else launch_block<D, 4, false>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+        } else {
+            if (vec) launch_block<D, 8, true>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+            else launch_block<D, 8, false>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+        }
+        return check_launch("decode_block_kernel");
+    }
     // the in-kernel final write is fp16 only; int8 rows always go through the combine
     const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
     if (vec && final_pass)
@@ -601,10 +778,14 @@ int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, con
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
     constexpr int NS = D == 128 ? 8 : 4;
     const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
+    const bool vec = aligned_to(sKp, 16) && aligned_to(sVp, 16);
 #define INT8K_PAGED_LAUNCH(FIN, FLV)                                                         \
-    decode_paged_kernel<D, NS, FIN, FLV><<<grid, kBlockThreads, 0, stream>>>(                \
+    if (vec) decode_paged_kernel<D, NS, FIN, FLV, true><<<grid, kBlockThreads, 0, stream>>>( \
         Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,     \
-        log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk)
+        log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk, tuning_for(D).stagger); \
+    else decode_paged_kernel<D, NS, FIN, FLV, false><<<grid, kBlockThreads, 0, stream>>>(   \
+        Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,     \
+        log2_page, max_pages, plan.nsplit, plan.chunk, (int)units, qk, tuning_for(D).stagger)
 #define INT8K_PAGED_FLAGS(FIN)                          \
     switch (tuning_for(D).flags & 3) {                  \
         case 0: INT8K_PAGED_LAUNCH(FIN, 0); break;      \

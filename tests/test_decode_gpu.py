@@ -60,17 +60,29 @@ def test_decode_check_cases(capi, gpu, B, H, D, S):
 
 @pytest.mark.parametrize("D", [64, 128])
 def test_decode_split_invariance(capi, gpu, D):
-    case = workloads.decode_case(3, 5, D, 1000, seed=7, device=gpu, gen_device="cpu")
+    # up to 16 chunks per (b,h) run as one launch (chunks merged in LDS), more as the
+    # split + combine pair: the result does not depend on the split count either way
+    case = workloads.decode_case(3, 5, D, 3000, seed=7, device=gpu, gen_device="cpu")
     ref = _oracle(case)
     outs = []
-    for ns in (1, 2, 3, 5, 8, 100):
-        got = capi.decode_num_splits(15, 1000, D, ns)
+    for ns in (1, 2, 3, 5, 8, 16, 17, 24, 100):
+        got = capi.decode_num_splits(15, 3000, D, ns)
         assert 1 <= got <= ns
         out = _run_capi(capi, case, nsplit=ns)
         assert_attn_close(out, ref, f"nsplit={ns}")
         outs.append(out)
     for o in outs[1:]:
         assert np.abs(o - outs[0]).max() <= 2e-3
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_decode_few_heads_long_context(capi, gpu, D):
+    # few (b,h) and a long context: the automatic plan has more than 16 chunks per
+    # (b,h), so it runs the split kernel and the combine kernel
+    case = workloads.decode_case(1, 2, D, 40000, seed=17, outlier_frac=0.01, device=gpu)
+    assert capi.decode_num_splits(2, 40000, D, 0) > 16
+    out = _run_capi(capi, case)
+    assert_attn_close(out, _oracle(case), f"B1 H2 D{D} S40000")
 
 
 @pytest.mark.parametrize("D", [64, 128])
