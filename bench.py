@@ -812,66 +812,11 @@ def bench_block(args):
     import torch.nn.functional as F
 
     import int8_ext as ext
-    import workloads
+    from block import TransformerBlock
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
-
-    class Block:
-        def __init__(self, d, H, dff):
-            self.d, self.H, self.Dh, self.dff = d, H, d // H, dff
-            g = torch.Generator(device=dev).manual_seed(0)
-            rn = lambda *sh: torch.randn(*sh, generator=g, device=dev, dtype=torch.float16)  # noqa: E731
-            self.Wqkv = rn(d, 3 * d) * (d ** -0.5)
-            self.Wo = rn(d, d) * (d ** -0.5)
-            self.W1 = rn(d, dff) * (d ** -0.5)
-            self.W2 = rn(dff, d) * (dff ** -0.5)
-            w1i, self.sW1 = workloads.quantize_per_channel_w(self.W1)
-            w2i, self.sW2 = workloads.quantize_per_channel_w(self.W2)
-            self.W1T, self.W2T = ext.transpose_int8_weights(w1i, w2i)
-
-        def mlp_int8_residual(self, h):
-            # h + MLP(LN2(h)); the int8 output's dequantization and the residual add are
-            # one pass (the reference: h + (out.float() * out_scale).half())
-            B, S, d = h.shape
-            xi, sx = ext.layernorm_quantize_per_token(h)
-            o, so = ext.int8_mlp_forward_prepacked(xi.view(B, S, d), self.W1T, self.W2T,
-                                                   sx.reshape(-1), self.sW1, self.sW2)
-            return ext.dequantize_per_token(o.view(B, S, d), so.view(B, S), residual=h)
-
-        def mlp_fp16(self, h):
-            return F.gelu(F.layer_norm(h, (self.d,)) @ self.W1, approximate="tanh") @ self.W2
-
-        def prefill(self, x, int8):
-            B, S, _ = x.shape
-            qkv = F.layer_norm(x, (self.d,)) @ self.Wqkv
-            if int8:
-                qi, sq, ki, sk, vi, sv = ext.quantize_heads(qkv, self.H)
-                # rows come out as [B, S, H, Dh], the projection's order: no transpose copy
-                a = ext.int8_attention_forward(qi, ki, vi, sq, sk, sv, out_bshd=True)
-                a = a.view(B, S, self.d)
-            else:
-                q, k, v = (t.view(B, S, self.H, self.Dh).transpose(1, 2).contiguous()
-                           for t in qkv.split(self.d, dim=-1))
-                a = F.scaled_dot_product_attention(q, k, v)
-                a = a.transpose(1, 2).contiguous().view(B, S, self.d)
-            h = x + a @ self.Wo
-            return self.mlp_int8_residual(h) if int8 else h + self.mlp_fp16(h)
-
-        def decode(self, x, kv, int8):
-            B = x.size(0)
-            q = (F.layer_norm(x, (self.d,)) @ self.Wqkv)[..., :self.d]
-            if int8:
-                Ki, Vi, sK, sV = kv
-                qi, sq = ext.quantize_per_token(q.reshape(B, self.H, self.Dh))
-                a = ext.int8_decode_attention_forward(qi, Ki, Vi, sq, sK, sV).view(B, 1, self.d)
-            else:
-                Kf, Vf = kv
-                a = F.scaled_dot_product_attention(q.view(B, self.H, 1, self.Dh), Kf, Vf)
-                a = a.transpose(1, 2).contiguous().view(B, 1, self.d)
-            h = x + a @ self.Wo
-            return self.mlp_int8_residual(h) if int8 else h + self.mlp_fp16(h)
 
     def cos(a, b):
         return F.cosine_similarity(a.float().flatten(), b.float().flatten(), dim=0).item()
@@ -879,7 +824,7 @@ def bench_block(args):
     rows = []
     H, Dh, dff = 16, 64, 4096
     d = H * Dh
-    blk = Block(d, H, dff)
+    blk = TransformerBlock(d, H, dff, dev)
     g = torch.Generator(device=dev).manual_seed(args.seed)
     for S in (512, 1024, 2048):
         x = torch.randn(8, S, d, generator=g, device=dev, dtype=torch.float16)
