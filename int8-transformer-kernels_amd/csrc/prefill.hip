@@ -63,15 +63,13 @@ struct Shape {
     static constexpr int kMinBlocks = D == 64 ? 2 : 1;  // 2 waves per SIMD at D <= 128
 };
 constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
-// How far (log2 units) a tile's max may exceed the running reference max before
-// O is rescaled: p <= 2^4 on the fast path.
-constexpr float kRescaleSlack = 4.0f;
-// P' = fp16(p * sV) is finite for p <= 2^4 only while sV <= 65504 / 2^4.  A
-// tile holding a larger sV (V rows of absmax above ~5.2e5, which fp32 and
-// bf16 sources allow) takes the slow path, where p <= 1 and P' overflows only
-// above sV = 65504, as the reference's P' does (kernels/int8_attention.cu:
-// 530-572).  The tile's flag is set when it is staged.
-constexpr float kFastMaxSv = 65504.0f / 16.0f;
+// The V scales are applied once per staged tile, V^T = fp16(v * sV * 2^-E), and
+// the probabilities enter the PV MFMA as P = fp16(p * 2^E), so
+// P . V^T = sum_j p_j v_j sV_j as the reference's fp16(p * sV) . fp16(v)
+// (kernels/int8_attention.cu:530-572).  E >= 0 is the (b,h)'s exponent that
+// keeps 127 * max|sV| * 2^-E <= 32768 (0 for V from fp16 data), so V^T is
+// finite wherever the reference's P' is; E <= kMaxVExp.
+constexpr int kMaxVExp = 11;
 
 // LDS position of key kk (0..63) of a tile inside a V^T row: keys
 // 16t + 8a + 4h + c are stored at 16t + 8h + 4a + c, so the 8 keys that lane
@@ -92,15 +90,14 @@ __device__ __forceinline__ int v_dim_group(int it) {
     return 4 * (it >> 6) + ((g & 1) << 1 | (g >> 1));
 }
 
-// One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16), scales,
-// and the tile's large-sV flag (kFastMaxSv).
+// One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16, the V
+// scales applied), the key scales sK.
 template <int D>
 struct Stage {
     static constexpr int kKStride = D + 16;  // bytes per K row
     static constexpr int kKBytes = kKV * kKStride;
     static constexpr int kVtBytes = D * kVtStride * 2;
-    static constexpr int kFlagOff = kKBytes + kVtBytes + 2 * kKV * 4;
-    static constexpr int kBytes = kFlagOff + 16;
+    static constexpr int kBytes = kKBytes + kVtBytes + kKV * 4;
     static constexpr int kKChunks = kKV * D / 16 / Shape<D>::kThreads;  // 16-B K chunks per thread
     static constexpr int kVItems = kKV * D / 16 / Shape<D>::kThreads;   // 4x4 V blocks per thread
     static_assert(kKChunks >= 1 && kKChunks * 16 * Shape<D>::kThreads == kKV * D, "K tile split");
@@ -113,9 +110,9 @@ struct Stage {
 // (dm < D) loads only the K chunks and V dim groups below dm and zeroes the
 // rest (kvalid, vvalid: bit n for item n).
 struct TileSrc {
-    __amdgpu_buffer_rsrc_t k, s;
+    __amdgpu_buffer_rsrc_t k, s, sv;
     v4i v;  // V descriptor with a typed format: 8_8_8_8 SSCALED (see load_v_f16x4)
-    uint32_t voff_k, voff_v, voff_s;
+    uint32_t voff_k, voff_v, voff_s, voff_sv;
     uint32_t kstep, dm;  // bytes between K chunks n and n+1; row stride in memory
     bool kvalid;
     uint32_t vvalid;
@@ -164,7 +161,9 @@ __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t
     src.dm = (uint32_t)dm;
     src.k = make_buffer(Kbh, (uint32_t)S * dm);
     src.v = make_v_descriptor(Vbh, (uint32_t)S * dm);
-    src.s = make_buffer(wave == 0 ? sKbh : sVbh, (uint32_t)S * 4);  // waves 0 and 1 load scales
+    (void)wave;
+    src.s = make_buffer(sKbh, (uint32_t)S * 4);    // wave 0 loads the tile's sK
+    src.sv = make_buffer(sVbh, (uint32_t)S * 4);   // every thread: sV of its 4 V keys
     const int kcol = (t % (D / 16)) * 16;
     src.voff_k = (t / (D / 16)) * dm + kcol;
     src.kstep = (uint32_t)(kT * 16 / D) * dm;  // chunk t + n kT is kT*16/D rows further
@@ -175,6 +174,7 @@ __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t
     for (int n = 0; n < Stage<D>::kVItems; ++n)
         if (4 * v_dim_group(t + n * kT) < dm) src.vvalid |= 1u << n;
     src.voff_s = (t & (kKV - 1)) * 4;
+    src.voff_sv = 4 * v_key_group(t) * 4;
     return src;
 }
 
@@ -183,7 +183,8 @@ template <int D>
 struct Prefetch {
     int4 k[Stage<D>::kKChunks];
     uint2 v[Stage<D>::kVItems][4];  // key 4 kg + i, dims 4 dg .. 4 dg + 3 as fp16 pairs
-    float sc;  // threads 0..63: sK of key tid; 64..127: sV of key tid-64
+    float4 sv;  // sV of keys 4 kg .. 4 kg + 3 (the same for every V item of a thread)
+    float sc;   // threads 0..63: sK of key tid
 };
 
 // Thread t (of kT) loads 16-byte K chunk t + kT n (row (t + kT n) / (D/16);
@@ -217,19 +218,20 @@ __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& sr
             for (int i = 0; i < 4; ++i) pf.v[n][i] = make_uint2(0, 0);
         }
     }
-    if (threadIdx.x < 2 * kKV)
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f sv = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(src.sv, src.voff_sv,
+                                                                                k0 * 4, 0));
+    pf.sv = make_float4(sv.x, sv.y, sv.z, sv.w);
+    if (threadIdx.x < kKV)
         pf.sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.s, src.voff_s,
                                                                                k0 * 4, 0));
 }
 
+// vscale = 2^-E: V^T = fp16(v * fp16(sV * 2^-E)) on v_pk_mul_f16.
 template <int D>
-__device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
+__device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st, float vscale) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const int t = threadIdx.x;
-    // wave 1 holds the tile's sV: flag a tile whose P' could overflow on the fast path
-    if (__builtin_amdgcn_readfirstlane(t >> 6) == 1) {
-        const bool big = __ballot(pf.sc > kFastMaxSv) != 0;
-        if (t == 64) *reinterpret_cast<int*>(st + Stage<D>::kFlagOff) = big ? 1 : 0;
-    }
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
         const int c = t + n * Shape<D>::kThreads;
@@ -244,7 +246,16 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
         const int it = t + n * Shape<D>::kThreads;
         const int kg = v_key_group(it), dg = v_dim_group(it);
         const int p0 = vt_pos(4 * kg);
-        const uint2* w = pf.v[n];
+        // key 4 kg + i scaled by its sV * 2^-E (both dims of a word share the key)
+        const float svk[4] = {pf.sv.x * vscale, pf.sv.y * vscale, pf.sv.z * vscale,
+                              pf.sv.w * vscale};
+        uint2 w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const h2 sp = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){svk[i], svk[i]}, h2);
+            w[i].x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pf.v[n][i].x) * sp);
+            w[i].y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pf.v[n][i].y) * sp);
+        }
         // dim 4 dg + j of keys 4 kg .. 4 kg + 3 -> 4 consecutive fp16 of V^T row 4 dg + j
         *reinterpret_cast<uint2*>(vt + (4 * dg + 0) * kVtStride + p0) =
             make_uint2(__builtin_amdgcn_perm(w[1].x, w[0].x, kLo),
@@ -259,8 +270,7 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st) {
             make_uint2(__builtin_amdgcn_perm(w[1].y, w[0].y, kHi),
                        __builtin_amdgcn_perm(w[3].y, w[2].y, kHi));
     }
-    if (t < 2 * kKV)
-        reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
+    if (t < kKV) reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
 }
 
 // D: the kernel's head_dim.  PAD: the rows in memory have head_dim d_mem < D
@@ -331,6 +341,32 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int n_kv = (kv_end + kKV - 1) / kKV;
     const int q_wave_last = min(qw0 + 31, S - 1);
 
+    // E: the exponent that keeps the scaled V^T in fp16 range, from max |sV| over
+    // the keys this block reads (a block-wide reduction through LDS).
+    __shared__ float s_svmax[Shape<D>::kWaves];
+    {
+        float a = 0.f;
+        for (int j = threadIdx.x; j < kv_end; j += Shape<D>::kThreads) a = fmaxf(a, fabsf(sVbh[j]));
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) a = fmaxf(a, __shfl_xor(a, off));
+        if (lane == 0) s_svmax[wave] = a;
+    }
+    __syncthreads();
+    float svmax = s_svmax[0];
+#pragma unroll
+    for (int w = 1; w < Shape<D>::kWaves; ++w) svmax = fmaxf(svmax, s_svmax[w]);
+    int vexp = 0;  // smallest E (up to kMaxVExp) with 127 max|sV| 2^-E <= 32768
+    {
+        const float need = svmax * (127.f / 32768.f);
+        if (!(need <= 1.f)) {
+            int e = kMaxVExp;
+            if (need < INFINITY) frexpf(need, &e);  // need < 2^e
+            vexp = min(e, kMaxVExp);
+        }
+    }
+    const float vscale = __builtin_ldexpf(1.f, -vexp);  // V^T = fp16(v * sV * 2^-E)
+    const float pexp = (float)vexp;                      // P = fp16(p * 2^E)
+
     // Pipeline: tile kt is computed from LDS stage kt&1.  The register set pf
     // holds tile kt+1 while tile kt is computed; at the end of the step it is
     // written to the other stage, refilled with tile kt+2, and the step's one
@@ -338,12 +374,12 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
     Prefetch<D> pf;
     prefetch_tile<D, PAD>(pf, src, 0);
-    commit_tile<D>(pf, smem);
+    commit_tile<D>(pf, smem, vscale);
     if (n_kv > 1) prefetch_tile<D, PAD>(pf, src, kKV);
     __syncthreads();
     auto advance = [&](int kt) {
         if (kt + 1 < n_kv) {
-            commit_tile<D>(pf, smem + ((kt + 1) & 1) * St::kBytes);
+            commit_tile<D>(pf, smem + ((kt + 1) & 1) * St::kBytes, vscale);
             if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pf, src, (kt + 2) * kKV);
         }
         // tile kt+1 is in LDS and every wave is done reading stage kt&1
@@ -382,26 +418,22 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     auto sk_of = [&](int kt) {
         return reinterpret_cast<const float*>(stage_of(kt) + St::kKBytes + St::kVtBytes);
     };
-    // the tile holds an sV above kFastMaxSv (wave-uniform)
-    auto sv_big = [&](int kt) {
-        return __builtin_amdgcn_readfirstlane(
-                   *reinterpret_cast<const int*>(stage_of(kt) + St::kFlagOff)) != 0;
-    };
     // A wave computes tile kt unless the causal mask hides all of it from the wave's queries.
     auto computes = [&](int kt) { return !(CAUSAL && kt * kKV > q_wave_last); };
 
     // Scores of this lane's 32 keys: key = k0 + 32T + 8g + 4h + c <-> sacc[T][4g + c];
-    // P'^T = p * sV (fp16): slice t = registers [8(t%2), 8(t%2)+8) of half t/2.
+    // P^T = fp16(p * 2^E): slice t = registers [8(t%2), 8(t%2)+8) of half t/2.
     //
-    // The running max m is a reference, not necessarily the exact running max: a
-    // tile takes the fast path when it has no masked key, every lane's qscale is
-    // >= 0, no sV of the tile exceeds kFastMaxSv and no lane's tile max exceeds
-    // m by more than kRescaleSlack (log2 units).  Then p = 2^(u*qscale - m) <= 2^kRescaleSlack, O is only updated by
-    // the PV MFMAs (in place), and the rescale is skipped.  Every other tile
-    // (first tile, masked edge and diagonal tiles, a large max increase) takes the
-    // slow path, which sets m to the exact running max and rescales O and l.
-    // The fast path runs as an inner loop that the slow path leaves and
-    // re-enters, so O has no conditional update inside it.
+    // The running max m is a reference, not necessarily the exact running max.  A
+    // tile takes the fast path when it has no masked key and every lane's qscale is
+    // >= 0: p = 2^(u*qscale - m + E) with the current m, no per-score max and no
+    // rescale of O; the tile is kept if each lane's sum of its 32 p stays below the
+    // fp16 maximum, so every P is finite.  p may exceed 1 when the scores have grown
+    // since m was set; O and l hold such values in fp32.  Every other tile (first
+    // tile, masked edge and diagonal tiles, a sum past the fp16 range) takes the slow
+    // path, which sets m to the exact running max and rescales O and l.  The fast
+    // path runs as an inner loop that the slow path leaves and re-enters, so O has
+    // no conditional update inside it.
     int kt = 0;
     while (kt < n_kv) {
         v16i sacc[2];
@@ -411,10 +443,11 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                 qk(kt, sacc);
                 const int k0 = kt * kKV;
                 const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
-                if (!(full && qpos) || sv_big(kt)) { slow = true; break; }
+                if (!(full && qpos)) { slow = true; break; }
                 const float* sk_l = sk_of(kt);
-                float u[2][16];
-                float mx = -INFINITY;
+                const float shift = pexp - m;
+                float tsum = 0.f;
+                v8h pfr[4];
 #pragma unroll
                 for (int T = 0; T < 2; ++T)
 #pragma unroll
@@ -423,28 +456,14 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                         const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
-                            u[T][4 * g + c] = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
-                            mx = fmaxf(mx, u[T][4 * g + c]);
+                            const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
+                            const float p = fast_exp2(fmaf(u, qscale, shift));
+                            tsum += p;
+                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)p;
                         }
                     }
-                mx = max_xor32(mx);
-                if (__ballot(!(mx * qscale <= m + kRescaleSlack))) { slow = true; break; }
-                const float neg_m = -m;
-                const float* sv_l = sk_l + kKV;
-                v8h pfr[4];
-#pragma unroll
-                for (int T = 0; T < 2; ++T)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float4 svv = *reinterpret_cast<const float4*>(sv_l + 32 * T + 8 * g + 4 * h);
-                        const float svk[4] = {svv.x, svv.y, svv.z, svv.w};
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            const float p = fast_exp2(fmaf(u[T][4 * g + c], qscale, neg_m));
-                            lsum += p;
-                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
-                        }
-                    }
+                if (__ballot(!(tsum <= 65504.f))) { slow = true; break; }
+                lsum += tsum;
                 pv(kt, pfr);
             }
             advance(kt);
@@ -455,7 +474,6 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
         {
             const int k0 = kt * kKV;
             const float* sk_l = sk_of(kt);
-            const float* sv_l = sk_l + kKV;
             float sc[2][16];
             float mx = -INFINITY;
 #pragma unroll
@@ -483,20 +501,18 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[t][r] *= corr;
             m = m_new;
+            const float shift = pexp - m_use;
             v8h pfr[4];
 #pragma unroll
             for (int T = 0; T < 2; ++T)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 svv = *reinterpret_cast<const float4*>(sv_l + 32 * T + 8 * g + 4 * h);
-                    const float svk[4] = {svv.x, svv.y, svv.z, svv.w};
+                for (int g = 0; g < 4; ++g)
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const float p = fast_exp2(sc[T][4 * g + c] - m_use);
+                        const float p = fast_exp2(sc[T][4 * g + c] + shift);
                         lsum += p;
-                        pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)(p * svk[c]);
+                        pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)p;
                     }
-                }
             pv(kt, pfr);
         }
         advance(kt);
@@ -505,7 +521,9 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
 
     const float L = sum_xor32(lsum);
     if (!qok) return;  // lanes l and l^32 share q, so both leave or both stay
-    const float inv = 1.f / L;
+    // l carries the 2^E of P; O = sum p v sV does not
+    float inv = 1.f / L;
+    if (vexp != 0) inv *= __builtin_ldexpf(1.f, vexp);
     // output row: [B, H, S, D] order, or [B, S, H, D] (the row order of the
     // output projection's input) with bshd
     const size_t orow_index =
