@@ -7,7 +7,8 @@ The default run (`--workload all`) measures every BASELINE configuration:
   * the headline, config 2: decode attention over a contiguous INT8 KV cache,
     B=32 H=32 D=128 ctx=8192 (2 GiB of K+V), 1% of channels x8 before
     per-token quantization.  One step = one decode call over the whole batch
-    (split kernel + combine kernel), inputs already resident in HBM.  Its
+    (one kernel launch: 8 chunks per (b,h) merged in LDS), inputs already
+    resident in HBM.  Its
     effective KV-read bandwidth (2*B*H*S*D bytes / step time, TB/s) is the
     line's `value`;
   * under `configs`: config 1 (B1 H12 D64 ctx 1K), config 3 (B8 H32 D64 ctx
@@ -216,9 +217,18 @@ def hbm_roofline(nbytes, ms, kernel, traffic_key=None, ceiling=None):
     return r
 
 
+def decode_kernel_label(nsplit):
+    """The kernels one contiguous decode step launches for a plan of `nsplit` chunks per
+    (b,h): up to 16 chunks run as one block each (merged in LDS), unless
+    INT8K_DECODE_BLOCK=0 turns that off."""
+    if nsplit <= 16 and os.environ.get("INT8K_DECODE_BLOCK", "1") != "0":
+        return "decode_block_kernel (one launch per step)"
+    return "decode_split_kernel + decode_combine_kernel (one step)"
+
+
 def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False):
     """One decode configuration: seeded inputs, `--warmup` untimed steps, then the median of
-    5 windows of `--steps` steps (split + combine).  Cases whose K+V (+ scales) are under
+    5 windows of `--steps` steps.  Cases whose K+V (+ scales) are under
     512 MB cycle through enough copies of the cache (at least 3, 768 MB in total) that the
     256 MB Infinity Cache cannot serve a step from the previous one.  Every (b,h) row of
     the output is checked against the C oracle."""
@@ -314,8 +324,8 @@ def bench_decode(args):
                    "kv_bytes": kv_bytes, "scale_bytes": 2 * B * H * S * 4,
                    "timing": f"median of {WINDOWS} windows of {args.steps} steps",
                    "windows_ms": row["windows_ms"], "parity": row["parity"]},
-        "roofline": hbm_roofline(kv_bytes, ms, "decode_split_kernel + decode_combine_kernel "
-                                 "(one step)", f"decode_b{B}h{H}d{D}_s{S}",
+        "roofline": hbm_roofline(kv_bytes, ms, decode_kernel_label(row["nsplit"]),
+                                 f"decode_b{B}h{H}d{D}_s{S}",
                                  round(ceilings["hbm_stream_read_TBps"] * 1e3, 1)
                                  if ceilings else None),
         "ceilings": ceilings,
@@ -378,7 +388,7 @@ def bench_decode_sweep(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("decode_b8h32d64_s32768"),
-                     "kernel": "decode_split_kernel + decode_combine_kernel (one step)"},
+                     "kernel": decode_kernel_label(head["nsplit"])},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_cfg1(cfg1_host),
     }
     return res
@@ -396,7 +406,7 @@ def sweep_rows(args, dev, stream):
         if host is not None:
             cfg1_host = host
         row["roofline"] = hbm_roofline(2 * B * H * S * D, row["us"] / 1e3,
-                                       "decode_split_kernel + decode_combine_kernel (one step)",
+                                       decode_kernel_label(row["nsplit"]),
                                        "decode_b8h32d64_s32768" if S == 32768 else None)
         rows.append(row)
         torch.cuda.empty_cache()
