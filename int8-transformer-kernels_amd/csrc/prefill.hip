@@ -13,7 +13,11 @@
 // and walks the KV sequence in tiles of 64 keys.  K (int8 rows), V (as fp16
 // V^T) and both key-scale vectors of a tile are staged in double-buffered LDS
 // by buffer loads: the next tile's loads are in flight in registers while the
-// current tile is computed, and there is one barrier per tile.  Everything is
+// current tile is computed, and there is one barrier per tile.  Causal grids
+// at head_dim <= 128 keep two tiles in flight (a second register set): all
+// heads are live at once there, so K/V come from beyond L2 and one step does
+// not cover the load latency.  The LDS reads of the MFMA fragments and key
+// scales are scheduled ahead of their uses.  Everything is
 // computed transposed so that each lane owns one query:
 //   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows
 //                                   from LDS, B = Q kept in VGPRs)
@@ -273,6 +277,21 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st, flo
     if (t < kKV) reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
 }
 
+// Sum of the 32 fp16 P of a lane in fp32 (v_dot2_f32_f16 against {1, 1}).
+__device__ __forceinline__ float psum(const v8h (&pfr)[4]) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one = {(_Float16)1.f, (_Float16)1.f};
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a = __builtin_amdgcn_fdot2(h2{pfr[i][0], pfr[i][1]}, one, a, false);
+        b = __builtin_amdgcn_fdot2(h2{pfr[i][2], pfr[i][3]}, one, b, false);
+        a = __builtin_amdgcn_fdot2(h2{pfr[i][4], pfr[i][5]}, one, a, false);
+        b = __builtin_amdgcn_fdot2(h2{pfr[i][6], pfr[i][7]}, one, b, false);
+    }
+    return a + b;
+}
+
 // D: the kernel's head_dim.  PAD: the rows in memory have head_dim d_mem < D
 // (a multiple of 16); the dims past it read as zero and are not stored.
 template <int D, bool CAUSAL, bool PAD>
@@ -341,6 +360,15 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int n_kv = (kv_end + kKV - 1) / kKV;
     const int q_wave_last = min(qw0 + 31, S - 1);
 
+    // Causal grids at D <= 128 keep two register sets of tiles in flight (their
+    // K/V come from further away: every head is live at once); the others one.
+    constexpr int kDepth = (CAUSAL && D <= 128) ? 2 : 1;
+    // The first tiles' loads go out before the exponent's reduction, so their
+    // latency overlaps it.
+    const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
+    Prefetch<D> pa, pb;
+    prefetch_tile<D, PAD>(pa, src, 0);
+
     // E: the exponent that keeps the scaled V^T in fp16 range, from max |sV| over
     // the keys this block reads (a block-wide reduction through LDS).
     __shared__ float s_svmax[Shape<D>::kWaves];
@@ -367,24 +395,6 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const float vscale = __builtin_ldexpf(1.f, -vexp);  // V^T = fp16(v * sV * 2^-E)
     const float pexp = (float)vexp;                      // P = fp16(p * 2^E)
 
-    // Pipeline: tile kt is computed from LDS stage kt&1.  The register set pf
-    // holds tile kt+1 while tile kt is computed; at the end of the step it is
-    // written to the other stage, refilled with tile kt+2, and the step's one
-    // barrier follows.
-    const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
-    Prefetch<D> pf;
-    prefetch_tile<D, PAD>(pf, src, 0);
-    commit_tile<D>(pf, smem, vscale);
-    if (n_kv > 1) prefetch_tile<D, PAD>(pf, src, kKV);
-    __syncthreads();
-    auto advance = [&](int kt) {
-        if (kt + 1 < n_kv) {
-            commit_tile<D>(pf, smem + ((kt + 1) & 1) * St::kBytes, vscale);
-            if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pf, src, (kt + 2) * kKV);
-        }
-        // tile kt+1 is in LDS and every wave is done reading stage kt&1
-        __syncthreads();
-    };
     auto stage_of = [&](int kt) { return smem + (kt & 1) * St::kBytes; };
     // S^T = K . Q^T for the two 32-key halves of tile kt
     auto qk = [&](int kt, v16i (&sacc)[2]) {
@@ -402,7 +412,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                 sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[s], qf[s], sacc[T], 0, 0, 0);
         }
     };
-    // O^T += V^T . P'^T
+    // O^T += V^T . P^T
     auto pv = [&](int kt, const v8h (&pfr)[4]) {
         const _Float16* vt = reinterpret_cast<const _Float16*>(stage_of(kt) + St::kKBytes);
 #pragma unroll
@@ -420,6 +430,38 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     };
     // A wave computes tile kt unless the causal mask hides all of it from the wave's queries.
     auto computes = [&](int kt) { return !(CAUSAL && kt * kKV > q_wave_last); };
+    // Tile kt has no key masked for any query of the wave.
+    auto full_tile = [&](int kt) {
+        const int k0 = kt * kKV;
+        return k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
+    };
+    // Keep the K-fragment and sK reads of the fast tile ahead of their uses
+    // (the compiler otherwise waits on each LDS read right before its MFMA).
+    auto schedule_qk = [&]() {
+#pragma unroll
+        for (int i = 0; i < NS; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+    };
+    // V^T fragments 4 MFMAs ahead of their use
+    auto schedule_pv = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 4 * NS - 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
 
     // Scores of this lane's 32 keys: key = k0 + 32T + 8g + 4h + c <-> sacc[T][4g + c];
     // P^T = fp16(p * 2^E): slice t = registers [8(t%2), 8(t%2)+8) of half t/2.
@@ -427,27 +469,172 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     // The running max m is a reference, not necessarily the exact running max.  A
     // tile takes the fast path when it has no masked key and every lane's qscale is
     // >= 0: p = 2^(u*qscale - m + E) with the current m, no per-score max and no
-    // rescale of O; the tile is kept if each lane's sum of its 32 p stays below the
+    // rescale of O; the tile is kept if each lane's sum of its 32 P stays below the
     // fp16 maximum, so every P is finite.  p may exceed 1 when the scores have grown
     // since m was set; O and l hold such values in fp32.  Every other tile (first
     // tile, masked edge and diagonal tiles, a sum past the fp16 range) takes the slow
-    // path, which sets m to the exact running max and rescales O and l.  The fast
-    // path runs as an inner loop that the slow path leaves and re-enters, so O has
-    // no conditional update inside it.
-    int kt = 0;
-    while (kt < n_kv) {
-        v16i sacc[2];
-        bool slow = false;
-        for (; kt < n_kv; ++kt) {
-            if (computes(kt)) {
+    // path, which sets m to the exact running max and rescales O and l.  l sums the
+    // fp16 P that enter the PV product.
+    auto softmax_fast = [&](int kt, const v16i (&sacc)[2], v8h (&pfr)[4]) {
+        const float* sk_l = sk_of(kt);
+        const float shift = pexp - m;
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
+                const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
+                    pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
+                        (_Float16)fast_exp2(fmaf(u, qscale, shift));
+                }
+            }
+        return psum(pfr);
+    };
+    auto softmax_slow = [&](int kt, const v16i (&sacc)[2], v8h (&pfr)[4]) {
+        const int k0 = kt * kKV;
+        const float* sk_l = sk_of(kt);
+        float sc[2][16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
+                const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int key = k0 + 32 * T + 8 * g + 4 * h + c;
+                    const bool masked = (key >= S) | (CAUSAL & (key > q));
+                    const float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
+                    sc[T][4 * g + c] = masked ? -INFINITY : v;
+                    mx = fmaxf(mx, sc[T][4 * g + c]);
+                }
+            }
+        mx = max_xor32(mx);
+        const float m_new = fmaxf(m, mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float corr = fast_exp2(m - m_use);
+#pragma unroll
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+        m = m_new;
+        const float shift = pexp - m_use;
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
+                        (_Float16)fast_exp2(sc[T][4 * g + c] + shift);
+        lsum = lsum * corr + psum(pfr);
+    };
+
+    if constexpr (kDepth == 2) {
+        // Tile kt is computed from LDS stage kt&1.  Two register sets alternate:
+        // during step kt, set kt&1 holds tile kt+1 (loaded two steps earlier) and
+        // the other set tile kt+2.  At the end of the step the set is written to
+        // the other stage and refilled with tile kt+3; one barrier per step.
+        commit_tile<D>(pa, smem, vscale);
+        if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, kKV);
+        if (n_kv > 2) prefetch_tile<D, PAD>(pb, src, 2 * kKV);
+        __syncthreads();
+        auto tile = [&](int kt) {
+            v16i sacc[2];
+            v8h pfr[4];
+            if (full_tile(kt) && qpos) {
                 qk(kt, sacc);
+                const float tsum = softmax_fast(kt, sacc, pfr);
+                schedule_qk();
+                if (__ballot(!(tsum <= 65504.f))) softmax_slow(kt, sacc, pfr);
+                else lsum += tsum;
+            } else {
+                qk(kt, sacc);
+                softmax_slow(kt, sacc, pfr);
+            }
+            pv(kt, pfr);
+            schedule_pv();
+        };
+        auto step = [&](int kt, Prefetch<D>& pfx) {
+            if (computes(kt)) tile(kt);
+            if (kt + 1 < n_kv) {
+                commit_tile<D>(pfx, smem + ((kt + 1) & 1) * St::kBytes, vscale);
+                if (kt + 3 < n_kv) prefetch_tile<D, PAD>(pfx, src, (kt + 3) * kKV);
+            }
+            __syncthreads();
+        };
+        for (int kt = 0; kt < n_kv; kt += 2) {
+            step(kt, pa);
+            if (kt + 1 < n_kv) step(kt + 1, pb);
+        }
+    } else {
+        // Tile kt is computed from LDS stage kt&1.  The register set holds tile
+        // kt+1 while tile kt is computed; at the end of the step it is written to
+        // the other stage, refilled with tile kt+2, and the step's one barrier
+        // follows.  The fast path runs as an inner loop that the slow path leaves
+        // and re-enters, so O has no conditional update inside it.
+        commit_tile<D>(pa, smem, vscale);
+        if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, kKV);
+        __syncthreads();
+        auto advance = [&](int kt) {
+            if (kt + 1 < n_kv) {
+                commit_tile<D>(pa, smem + ((kt + 1) & 1) * St::kBytes, vscale);
+                if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pa, src, (kt + 2) * kKV);
+            }
+            // tile kt+1 is in LDS and every wave is done reading stage kt&1
+            __syncthreads();
+        };
+        int kt = 0;
+        while (kt < n_kv) {
+            v16i sacc[2];
+            bool slow = false;
+            for (; kt < n_kv; ++kt) {
+                if (computes(kt)) {
+                    const int k0 = kt * kKV;
+                    const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
+                    if (!(full && qpos)) {
+                        qk(kt, sacc);
+                        slow = true;
+                        break;
+                    }
+                    qk(kt, sacc);
+                    const float* sk_l = sk_of(kt);
+                    const float shift = pexp - m;
+                    v8h pfr[4];
+#pragma unroll
+                    for (int T = 0; T < 2; ++T)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
+                            const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
+                                pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
+                                    (_Float16)fast_exp2(fmaf(u, qscale, shift));
+                            }
+                        }
+                    schedule_qk();
+                    const float tsum = psum(pfr);
+                    if (__ballot(!(tsum <= 65504.f))) { slow = true; break; }
+                    lsum += tsum;
+                    pv(kt, pfr);
+                    schedule_pv();
+                }
+                advance(kt);
+            }
+            if (!slow) break;
+            // Slow path for tile kt (its S^T is in sacc): s = acc * qscale * sK with masked
+            // keys at -inf, exact running max, rescale of O and l.
+            {
                 const int k0 = kt * kKV;
-                const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
-                if (!(full && qpos)) { slow = true; break; }
                 const float* sk_l = sk_of(kt);
-                const float shift = pexp - m;
-                float tsum = 0.f;
-                v8h pfr[4];
+                float sc[2][16];
+                float mx = -INFINITY;
 #pragma unroll
                 for (int T = 0; T < 2; ++T)
 #pragma unroll
@@ -456,67 +643,39 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                         const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
-                            const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
-                            const float p = fast_exp2(fmaf(u, qscale, shift));
-                            tsum += p;
-                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)p;
+                            float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
+                            const int key = k0 + 32 * T + 8 * g + 4 * h + c;
+                            if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
+                            sc[T][4 * g + c] = v;
+                            mx = fmaxf(mx, v);
                         }
                     }
-                if (__ballot(!(tsum <= 65504.f))) { slow = true; break; }
-                lsum += tsum;
+                mx = max_xor32(mx);
+                const float m_new = fmaxf(m, mx);
+                const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+                const float corr = fast_exp2(m - m_use);
+                lsum *= corr;
+#pragma unroll
+                for (int t = 0; t < NS; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+                m = m_new;
+                const float shift = pexp - m_use;
+                v8h pfr[4];
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
+                                (_Float16)fast_exp2(sc[T][4 * g + c] + shift);
+                lsum += psum(pfr);
                 pv(kt, pfr);
             }
             advance(kt);
+            ++kt;
         }
-        if (!slow) break;
-        // Slow path for tile kt (its S^T is in sacc): s = acc * qscale * sK with masked
-        // keys at -inf, exact running max, rescale of O and l.
-        {
-            const int k0 = kt * kKV;
-            const float* sk_l = sk_of(kt);
-            float sc[2][16];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int T = 0; T < 2; ++T)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
-                    const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
-                        const int key = k0 + 32 * T + 8 * g + 4 * h + c;
-                        if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
-                        sc[T][4 * g + c] = v;
-                        mx = fmaxf(mx, v);
-                    }
-                }
-            mx = max_xor32(mx);
-            const float m_new = fmaxf(m, mx);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float corr = fast_exp2(m - m_use);
-            lsum *= corr;
-#pragma unroll
-            for (int t = 0; t < NS; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-            m = m_new;
-            const float shift = pexp - m_use;
-            v8h pfr[4];
-#pragma unroll
-            for (int T = 0; T < 2; ++T)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const float p = fast_exp2(sc[T][4 * g + c] + shift);
-                        lsum += p;
-                        pfr[2 * T + (g >> 1)][4 * (g & 1) + c] = (_Float16)p;
-                    }
-            pv(kt, pfr);
-        }
-        advance(kt);
-        ++kt;
     }
 
     const float L = sum_xor32(lsum);
