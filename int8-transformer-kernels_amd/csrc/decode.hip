@@ -91,11 +91,12 @@ inline int env_int(const char* name, int dflt) {
 }
 
 // Defaults measured on MI355X at the BASELINE shapes (B32 H32 D128 8K and
-// B8 H32 D64 32K): D=128 — 8 slots, non-temporal K/V loads, ~8192 units (two
-// resident rounds at 16 waves/CU); D=64 — 4 slots, non-temporal scale loads,
-// ~1024 longer units.  Both rotate each unit's starting iteration (stagger),
-// which was worth 2-5%.  The INT8K_DECODE_* variables override these for
-// tuning sweeps (read once per process).
+// B8 H32 D64 2K..32K): D=128 — 8 slots, non-temporal K/V loads, ~8192 units
+// (two resident rounds at 16 waves/CU); D=64 — 4 slots, non-temporal scale
+// loads, ~2048 units (8 chunks per (b,h) at B8 H32: two waves per SIMD).
+// Both rotate each unit's starting iteration (stagger), which was worth 2-5%.
+// The INT8K_DECODE_* variables override these for tuning sweeps (read once
+// per process).
 DecodeTuning tuning_for(int D) {
     static const int e_slots = env_int("INT8K_DECODE_SLOTS", 0);
     static const int e_flags = env_int("INT8K_DECODE_FLAGS", -1);
@@ -103,7 +104,7 @@ DecodeTuning tuning_for(int D) {
     static const int e_stagger = env_int("INT8K_DECODE_STAGGER", -1);
     DecodeTuning t;
     if (D == 128) t = DecodeTuning{8, kNtKV, 8192, 1};
-    else t = DecodeTuning{4, kNtScales, 1024, 1};
+    else t = DecodeTuning{4, kNtScales, 2048, 1};
     if (e_slots == 4 || e_slots == 8) t.slots = e_slots;
     if (e_flags >= 0) t.flags = e_flags & 3;
     if (e_units > 0) t.target_units = e_units;
@@ -224,6 +225,49 @@ __device__ __forceinline__ void decode_math(const Int4 (&kv)[NS], const Int4 (&v
     m = m_new;
 }
 
+// The registers of one wave iteration: NSLOT rows per group of K, V and scales.
+template <int NS>
+struct IterBuf {
+    Int4 kv[NS], vv[NS];
+    float sk[NS], sv[NS];
+};
+
+// The loads of an unmasked wave iteration whose group rows start at row0.
+template <int D, int NS, bool VEC_SCALES, int FL>
+__device__ __forceinline__ void load_iter(IterBuf<NS>& b, const int8_t* __restrict__ Kbh,
+                                          const int8_t* __restrict__ Vbh,
+                                          const float* __restrict__ sKbh,
+                                          const float* __restrict__ sVbh, int row0, int sub) {
+    const int8_t* kp = Kbh + (size_t)row0 * D + sub * 16;
+    const int8_t* vp = Vbh + (size_t)row0 * D + sub * 16;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) b.kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * D);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) b.vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * D);
+    if constexpr (VEC_SCALES) {
+#pragma unroll
+        for (int t = 0; t < NS; t += 4) {
+            typedef float v4f __attribute__((ext_vector_type(4)));
+            v4f a, c;
+            if constexpr ((FL & kNtScales) != 0) {
+                a = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sKbh + row0 + t));
+                c = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sVbh + row0 + t));
+            } else {
+                a = *reinterpret_cast<const v4f*>(sKbh + row0 + t);
+                c = *reinterpret_cast<const v4f*>(sVbh + row0 + t);
+            }
+            b.sk[t] = a.x; b.sk[t + 1] = a.y; b.sk[t + 2] = a.z; b.sk[t + 3] = a.w;
+            b.sv[t] = c.x; b.sv[t + 1] = c.y; b.sv[t + 2] = c.z; b.sv[t + 3] = c.w;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            b.sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + row0 + t);
+            b.sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + row0 + t);
+        }
+    }
+}
+
 // One wave iteration over NSLOT rows per group.  MASKED handles the last
 // partial block of a chunk: rows >= j1 get score -inf and weight 0 (their
 // loads are redirected to row j1-1, which is in bounds).
@@ -233,50 +277,20 @@ __device__ __forceinline__ void decode_iter(
     const float* __restrict__ sKbh, const float* __restrict__ sVbh,
     int row0, int j1, int sub, const Int4& q, float qscale,
     float& m, float& l, float* acc) {
-    Int4 kv[NS], vv[NS];
-    float sk[NS], sv[NS];
-
+    IterBuf<NS> b;
     if constexpr (!MASKED) {
-        const int8_t* kp = Kbh + (size_t)row0 * D + sub * 16;
-        const int8_t* vp = Vbh + (size_t)row0 * D + sub * 16;
-#pragma unroll
-        for (int t = 0; t < NS; ++t) kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * D);
-#pragma unroll
-        for (int t = 0; t < NS; ++t) vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * D);
-        if constexpr (VEC_SCALES) {
-#pragma unroll
-            for (int t = 0; t < NS; t += 4) {
-                typedef float v4f __attribute__((ext_vector_type(4)));
-                v4f a, b;
-                if constexpr ((FL & kNtScales) != 0) {
-                    a = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sKbh + row0 + t));
-                    b = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(sVbh + row0 + t));
-                } else {
-                    a = *reinterpret_cast<const v4f*>(sKbh + row0 + t);
-                    b = *reinterpret_cast<const v4f*>(sVbh + row0 + t);
-                }
-                sk[t] = a.x; sk[t + 1] = a.y; sk[t + 2] = a.z; sk[t + 3] = a.w;
-                sv[t] = b.x; sv[t + 1] = b.y; sv[t + 2] = b.z; sv[t + 3] = b.w;
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < NS; ++t) {
-                sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + row0 + t);
-                sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + row0 + t);
-            }
-        }
+        load_iter<D, NS, VEC_SCALES, FL>(b, Kbh, Vbh, sKbh, sVbh, row0, sub);
     } else {
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
             const int r = min(row0 + t, j1 - 1);
-            kv[t] = load_kv16<(FL & kNtKV) != 0>(Kbh + (size_t)r * D + sub * 16);
-            vv[t] = load_kv16<(FL & kNtKV) != 0>(Vbh + (size_t)r * D + sub * 16);
-            sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + r);
-            sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + r);
+            b.kv[t] = load_kv16<(FL & kNtKV) != 0>(Kbh + (size_t)r * D + sub * 16);
+            b.vv[t] = load_kv16<(FL & kNtKV) != 0>(Vbh + (size_t)r * D + sub * 16);
+            b.sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + r);
+            b.sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + r);
         }
     }
-
-    decode_math<D, NS, MASKED>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
+    decode_math<D, NS, MASKED>(b.kv, b.vv, b.sk, b.sv, row0, j1, q, qscale, m, l, acc);
 }
 
 // Merges the G row-group states of a wave (lanes with equal `sub`) and writes
@@ -455,9 +469,14 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 // the split kernel does, merges its row groups and leaves (m, l, acc[D]) in
 // LDS; wave 0 then merges the chunks with the log-sum-exp rule and writes the
 // row.  No partial state leaves the chip and there is no second launch.
+// MAXW: the most waves the instance is launched with (8 or kMaxBlockSplits).
+// The 8-wave instance has twice the registers per wave, which lets NSLOT = 4
+// keep the next iteration's loads in flight (a second register set) while the
+// current one computes: a short chunk is only a few dependent load rounds, so
+// their latency would show.
 
-template <int D, int NS, bool VEC_SCALES, int FL>
-__global__ __launch_bounds__(64 * kMaxBlockSplits) void decode_block_kernel(
+template <int D, int NS, bool VEC_SCALES, int FL, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void decode_block_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K,
     const int8_t* __restrict__ V, const float* __restrict__ sQ,
     const float* __restrict__ sK, const float* __restrict__ sV, uint16_t* __restrict__ out,
@@ -465,8 +484,8 @@ __global__ __launch_bounds__(64 * kMaxBlockSplits) void decode_block_kernel(
     float qk_scale_log2, int stagger) {
     using G = DecodeGeom<D, NS>;
     constexpr int LPR = D / 16;
-    __shared__ float s_ml[kMaxBlockSplits][2];
-    __shared__ __align__(16) float s_acc[kMaxBlockSplits][D];
+    __shared__ float s_ml[MAXW][2];
+    __shared__ __align__(16) float s_acc[MAXW][D];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
@@ -490,11 +509,38 @@ __global__ __launch_bounds__(64 * kMaxBlockSplits) void decode_block_kernel(
     const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
     const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
     int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
-    for (int k = 0; k < n_full; ++k) {
-        decode_iter<D, NS, false, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh,
-                                                  j0 + it * G::kRowsPerIter + grp * NS, j1, sub,
-                                                  q, qscale_l, m, l, acc);
-        it = (it + 1 == n_full) ? 0 : it + 1;
+    auto row_of = [&](int i) { return j0 + i * G::kRowsPerIter + grp * NS; };
+    auto nxt = [&](int i) { return (i + 1 == n_full) ? 0 : i + 1; };
+    if constexpr (MAXW <= 8 && NS == 4) {
+        // two register sets: iteration k+1's loads are issued before iteration k
+        // is computed (the fences keep the compiler from sinking them)
+        IterBuf<NS> ba, bb;
+        if (n_full > 0) load_iter<D, NS, VEC_SCALES, FL>(ba, Kbh, Vbh, sKbh, sVbh, row_of(it), sub);
+        int k = 0;
+        for (; k + 2 < n_full; k += 2) {
+            const int it1 = nxt(it);
+            load_iter<D, NS, VEC_SCALES, FL>(bb, Kbh, Vbh, sKbh, sVbh, row_of(it1), sub);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, j1, q, qscale_l, m, l, acc);
+            it = nxt(it1);
+            load_iter<D, NS, VEC_SCALES, FL>(ba, Kbh, Vbh, sKbh, sVbh, row_of(it), sub);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, j1, q, qscale_l, m, l, acc);
+        }
+        if (n_full - k == 2) {
+            load_iter<D, NS, VEC_SCALES, FL>(bb, Kbh, Vbh, sKbh, sVbh, row_of(nxt(it)), sub);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, j1, q, qscale_l, m, l, acc);
+            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, j1, q, qscale_l, m, l, acc);
+        } else if (n_full - k == 1) {
+            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, j1, q, qscale_l, m, l, acc);
+        }
+    } else {
+        for (int k = 0; k < n_full; ++k) {
+            decode_iter<D, NS, false, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, row_of(it), j1, sub, q,
+                                                      qscale_l, m, l, acc);
+            it = nxt(it);
+        }
     }
     const int base = j0 + n_full * G::kRowsPerIter;
     if (base < j1)
@@ -689,9 +735,14 @@ void launch_block(int flags, int stagger, int BH, hipStream_t stream, const int8
                   const int8_t* K, const int8_t* V, const float* sQ, const float* sK,
                   const float* sV, uint16_t* out, int8_t* qout, float* qs, int S, int S_cap,
                   const SplitPlan& plan, float qk) {
-#define INT8K_BLOCK_LAUNCH(FLV)                                                             \
-    decode_block_kernel<D, NS, VEC, FLV><<<(unsigned)BH, 64 * plan.nsplit, 0, stream>>>(    \
-        Q, K, V, sQ, sK, sV, out, qout, qs, S, S_cap, plan.chunk, qk, stagger)
+#define INT8K_BLOCK_LAUNCH(FLV)                                                               \
+    if (plan.nsplit <= 8)                                                                     \
+        decode_block_kernel<D, NS, VEC, FLV, 8><<<(unsigned)BH, 64 * plan.nsplit, 0, stream>>>(  \
+            Q, K, V, sQ, sK, sV, out, qout, qs, S, S_cap, plan.chunk, qk, stagger);           \
+    else                                                                                      \
+        decode_block_kernel<D, NS, VEC, FLV, kMaxBlockSplits>                                 \
+            <<<(unsigned)BH, 64 * plan.nsplit, 0, stream>>>(Q, K, V, sQ, sK, sV, out, qout, qs, \
+                                                            S, S_cap, plan.chunk, qk, stagger)
     switch (flags & 3) {
         case 0: INT8K_BLOCK_LAUNCH(0); break;
         case 1: INT8K_BLOCK_LAUNCH(1); break;

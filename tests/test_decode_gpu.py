@@ -76,6 +76,21 @@ def test_decode_split_invariance(capi, gpu, D):
 
 
 @pytest.mark.parametrize("D", [64, 128])
+def test_decode_chunk_iteration_counts(capi, gpu, D):
+    # chunks of 0..9 whole wave iterations plus masked tails, at 1, 2, 3 and 8 chunks
+    # per (b,h): at D=64 these take the one-launch kernel's two-register-set loop
+    # (every parity of the iteration count, the rotated start, the last pair)
+    rows = 64  # rows per wave iteration at the default slots, both head dims
+    for S in (1, 40, rows, rows + 9, 2 * rows, 3 * rows - 1, 3 * rows, 5 * rows + 17, 9 * rows,
+              19 * rows + 3):
+        case = workloads.decode_case(2, 3, D, S, seed=S, device=gpu, gen_device="cpu")
+        ref = _oracle(case)
+        for ns in (1, 2, 3, 8):
+            out = _run_capi(capi, case, nsplit=ns)
+            assert_attn_close(out, ref, f"D{D} S{S} nsplit={ns}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
 def test_decode_few_heads_long_context(capi, gpu, D):
     # few (b,h) and a long context: the automatic plan has more than 16 chunks per
     # (b,h), so it runs the split kernel and the combine kernel
