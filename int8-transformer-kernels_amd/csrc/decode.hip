@@ -74,6 +74,9 @@ struct SplitPlan {
 // Most chunks per (b,h) that run as one launch (decode_block_kernel: one wave
 // per chunk, merged in LDS); larger plans run the split + combine pair.
 constexpr int kMaxBlockSplits = 16;
+// Largest page-id table the paged one-launch kernel stages in LDS (12288 ids);
+// longer tables run the paged split + combine pair.
+constexpr long long kPagedLdsTableBytes = 48 << 10;
 
 // Plans of at most kMaxBlockSplits chunks run as one launch (decode_block_kernel);
 // INT8K_DECODE_BLOCK=0 keeps them on the split + combine pair (read once).
@@ -237,7 +240,7 @@ template <int D, int NS, bool VEC_SCALES, int FL>
 __device__ __forceinline__ void load_iter(IterBuf<NS>& b, const int8_t* __restrict__ Kbh,
                                           const int8_t* __restrict__ Vbh,
                                           const float* __restrict__ sKbh,
-                                          const float* __restrict__ sVbh, int row0, int sub) {
+                                          const float* __restrict__ sVbh, size_t row0, int sub) {
     const int8_t* kp = Kbh + (size_t)row0 * D + sub * 16;
     const int8_t* vp = Vbh + (size_t)row0 * D + sub * 16;
 #pragma unroll
@@ -464,6 +467,106 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
     emit_row<D>(acc, L, lane, bh, out, qout, qscale);
 }
 
+// The n_full whole iterations of a wave's chunk, starting at iteration `it` and
+// wrapping around.  roff(i): the row offset (from the K/V/scale bases) of the
+// group's first row in iteration i.  PIPE: two register sets, iteration
+// k+1's loads issued before iteration k is computed (the fences keep the
+// compiler from sinking them).
+template <int D, int NS, bool VEC_SCALES, int FL, bool PIPE, typename RowOff>
+__device__ __forceinline__ void walk_iters(const int8_t* __restrict__ K,
+                                           const int8_t* __restrict__ V,
+                                           const float* __restrict__ sK,
+                                           const float* __restrict__ sV, RowOff roff, int n_full,
+                                           int it, int sub, const Int4& q, float qscale, float& m,
+                                           float& l, float* acc) {
+    auto nxt = [&](int i) { return (i + 1 == n_full) ? 0 : i + 1; };
+    if constexpr (PIPE) {
+        IterBuf<NS> ba, bb;
+        if (n_full > 0) load_iter<D, NS, VEC_SCALES, FL>(ba, K, V, sK, sV, roff(it), sub);
+        int k = 0;
+        for (; k + 2 < n_full; k += 2) {
+            const int it1 = nxt(it);
+            load_iter<D, NS, VEC_SCALES, FL>(bb, K, V, sK, sV, roff(it1), sub);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, 0, q, qscale, m, l, acc);
+            it = nxt(it1);
+            load_iter<D, NS, VEC_SCALES, FL>(ba, K, V, sK, sV, roff(it), sub);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, 0, q, qscale, m, l, acc);
+        }
+        if (n_full - k == 2) {
+            load_iter<D, NS, VEC_SCALES, FL>(bb, K, V, sK, sV, roff(nxt(it)), sub);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, 0, q, qscale, m, l, acc);
+            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, 0, q, qscale, m, l, acc);
+        } else if (n_full - k == 1) {
+            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, 0, q, qscale, m, l, acc);
+        }
+    } else {
+        for (int k = 0; k < n_full; ++k) {
+            IterBuf<NS> b;
+            load_iter<D, NS, VEC_SCALES, FL>(b, K, V, sK, sV, roff(it), sub);
+            decode_math<D, NS, false>(b.kv, b.vv, b.sk, b.sv, 0, 0, q, qscale, m, l, acc);
+            it = nxt(it);
+        }
+    }
+}
+
+// The end of a one-launch block: each wave merges its row groups (lanes with
+// equal `sub`) and leaves (M, L, acc[D]) in LDS; wave 0 merges the nw chunk
+// states with the log-sum-exp rule, as decode_combine_kernel, and writes the
+// row.  Every wave of the block calls it (it holds the block's barrier).
+template <int D, int MAXW>
+__device__ __forceinline__ void merge_block(float m, float l, float* acc, int lane, int grp,
+                                            int sub, int w, int nw, int bh,
+                                            float (&s_ml)[MAXW][2], float (&s_acc)[MAXW][D],
+                                            uint16_t* __restrict__ out,
+                                            int8_t* __restrict__ qout,
+                                            float* __restrict__ qscale) {
+    constexpr int LPR = D / 16;
+    float M = m;
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+    const float f = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
+    float Lw = l * f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= f;
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+        Lw += __shfl_xor(Lw, off);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
+    }
+    if (grp == 0) {
+        float4* dst = reinterpret_cast<float4*>(&s_acc[w][sub * 16]);
+        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+        dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
+        if (sub == 0) {
+            s_ml[w][0] = M;
+            s_ml[w][1] = Lw;
+        }
+    }
+    __syncthreads();
+    if (w != 0) return;
+    constexpr int DPL = D / 64;
+    float Mall = -INFINITY;
+    for (int c = 0; c < nw; ++c) Mall = fmaxf(Mall, s_ml[c][0]);
+    const float M_use = (Mall == -INFINITY) ? 0.f : Mall;
+    float L = 0.f;
+    float o[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+    for (int c = 0; c < nw; ++c) {
+        const float wt = fast_exp2(s_ml[c][0] - M_use);
+        L += s_ml[c][1] * wt;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] = fmaf(s_acc[c][lane * DPL + i], wt, o[i]);
+    }
+    emit_row<D>(o, L, lane, bh, out, qout, qscale);
+}
+
 // One launch for plans of at most kMaxBlockSplits chunks per (b,h): block bh
 // runs one wave per chunk (blockDim.x / 64 waves), each wave walks its chunk as
 // the split kernel does, merges its row groups and leaves (m, l, acc[D]) in
@@ -474,7 +577,6 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 // keep the next iteration's loads in flight (a second register set) while the
 // current one computes: a short chunk is only a few dependent load rounds, so
 // their latency would show.
-
 template <int D, int NS, bool VEC_SCALES, int FL, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void decode_block_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K,
@@ -508,88 +610,83 @@ __global__ __launch_bounds__(64 * MAXW) void decode_block_kernel(
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
     const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
-    int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
-    auto row_of = [&](int i) { return j0 + i * G::kRowsPerIter + grp * NS; };
-    auto nxt = [&](int i) { return (i + 1 == n_full) ? 0 : i + 1; };
-    if constexpr (MAXW <= 8 && NS == 4) {
-        // two register sets: iteration k+1's loads are issued before iteration k
-        // is computed (the fences keep the compiler from sinking them)
-        IterBuf<NS> ba, bb;
-        if (n_full > 0) load_iter<D, NS, VEC_SCALES, FL>(ba, Kbh, Vbh, sKbh, sVbh, row_of(it), sub);
-        int k = 0;
-        for (; k + 2 < n_full; k += 2) {
-            const int it1 = nxt(it);
-            load_iter<D, NS, VEC_SCALES, FL>(bb, Kbh, Vbh, sKbh, sVbh, row_of(it1), sub);
-            __builtin_amdgcn_sched_barrier(0);
-            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, j1, q, qscale_l, m, l, acc);
-            it = nxt(it1);
-            load_iter<D, NS, VEC_SCALES, FL>(ba, Kbh, Vbh, sKbh, sVbh, row_of(it), sub);
-            __builtin_amdgcn_sched_barrier(0);
-            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, j1, q, qscale_l, m, l, acc);
-        }
-        if (n_full - k == 2) {
-            load_iter<D, NS, VEC_SCALES, FL>(bb, Kbh, Vbh, sKbh, sVbh, row_of(nxt(it)), sub);
-            __builtin_amdgcn_sched_barrier(0);
-            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, j1, q, qscale_l, m, l, acc);
-            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, j1, q, qscale_l, m, l, acc);
-        } else if (n_full - k == 1) {
-            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, j1, q, qscale_l, m, l, acc);
-        }
-    } else {
-        for (int k = 0; k < n_full; ++k) {
-            decode_iter<D, NS, false, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, row_of(it), j1, sub, q,
-                                                      qscale_l, m, l, acc);
-            it = nxt(it);
-        }
-    }
+    const int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
+    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4)>(
+        Kbh, Vbh, sKbh, sVbh, [&](int i) { return (size_t)(j0 + i * G::kRowsPerIter + grp * NS); },
+        n_full, it, sub, q, qscale_l, m, l, acc);
     const int base = j0 + n_full * G::kRowsPerIter;
     if (base < j1)
         decode_iter<D, NS, true, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, base + grp * NS, j1, sub,
                                                  q, qscale_l, m, l, acc);
+    merge_block<D, MAXW>(m, l, acc, lane, grp, sub, w, nw, bh, s_ml, s_acc, out, qout, qscale);
+}
 
-    // merge the wave's row groups (lanes with equal `sub`)
-    float M = m;
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
-    const float f = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
-    float Lw = l * f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] *= f;
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-        Lw += __shfl_xor(Lw, off);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] += __shfl_xor(acc[e], off);
-    }
-    if (grp == 0) {
-        float4* dst = reinterpret_cast<float4*>(&s_acc[w][sub * 16]);
-        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-        dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
-        dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
-        if (sub == 0) {
-            s_ml[w][0] = M;
-            s_ml[w][1] = Lw;
-        }
-    }
+// Paged one-launch variant for plans of up to 8 chunks per (b,h): the block
+// of (b,h) first copies sequence b's page ids (the first n_tab, clamped to
+// [0, num_pages) as in decode_paged_kernel) into LDS, so that each
+// iteration's row offset is an LDS read instead of a global load in front of
+// its K/V loads; then it walks and merges its chunks as decode_block_kernel.
+template <int D, int NS, bool VEC_SCALES, int FL, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void decode_paged_block_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ Kp,
+    const int8_t* __restrict__ Vp, const float* __restrict__ sQ,
+    const float* __restrict__ sKp, const float* __restrict__ sVp,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    uint16_t* __restrict__ out, int8_t* __restrict__ qout, float* __restrict__ qscale, int H,
+    int num_pages, int log2_page, int max_pages, int n_tab, int chunk, float qk_scale_log2,
+    int stagger) {
+    using G = DecodeGeom<D, NS>;
+    constexpr int LPR = D / 16;
+    extern __shared__ int s_pages[];
+    __shared__ float s_ml[MAXW][2];
+    __shared__ __align__(16) float s_acc[MAXW][D];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int bh = blockIdx.x;
+    const int b = bh / H, hh = bh - b * H;
+    const int page = 1 << log2_page;
+    const int32_t* table = block_tables + (size_t)b * max_pages;
+    for (int i = threadIdx.x; i < n_tab; i += blockDim.x)
+        s_pages[i] = (int)min((unsigned)table[i], (unsigned)(num_pages - 1));
     __syncthreads();
-    if (w != 0) return;
-    // wave 0: the log-sum-exp merge of the chunks, as decode_combine_kernel
-    constexpr int DPL = D / 64;
-    float Mall = -INFINITY;
-    for (int c = 0; c < nw; ++c) Mall = fmaxf(Mall, s_ml[c][0]);
-    const float M_use = (Mall == -INFINITY) ? 0.f : Mall;
-    float L = 0.f;
-    float o[DPL];
+    const int len = min(context_lens[b], n_tab << log2_page);
+    const int j0 = w * chunk;
+    const int j1 = min(len, j0 + chunk);
+    const int sub = lane % LPR;
+    const int grp = lane / LPR;
+    const Int4 q = load16(Q + (size_t)bh * D + sub * 16);
+    const float qscale_l = sQ[bh] * qk_scale_log2;
+    // row offset (in rows of the page arrays) of position r of this head
+    auto row_off = [&](int r) -> size_t {
+        return ((size_t)s_pages[r >> log2_page] * H + hh) * page + (r & (page - 1));
+    };
+
+    float m = -INFINITY, l = 0.f;
+    float acc[16];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) o[i] = 0.f;
-    for (int c = 0; c < nw; ++c) {
-        const float wt = fast_exp2(s_ml[c][0] - M_use);
-        L += s_ml[c][1] * wt;
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
+    const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
+    const int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
+    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4)>(
+        Kp, Vp, sKp, sVp, [&](int i) { return row_off(j0 + i * G::kRowsPerIter + grp * NS); },
+        n_full, it, sub, q, qscale_l, m, l, acc);
+    const int base = j0 + n_full * G::kRowsPerIter;
+    if (base < j1) {
+        const int row0 = base + grp * NS;
+        IterBuf<NS> bt;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) o[i] = fmaf(s_acc[c][lane * DPL + i], wt, o[i]);
+        for (int t = 0; t < NS; ++t) {
+            const size_t r = row_off(min(row0 + t, j1 - 1));
+            bt.kv[t] = load_kv16<(FL & kNtKV) != 0>(Kp + r * D + sub * 16);
+            bt.vv[t] = load_kv16<(FL & kNtKV) != 0>(Vp + r * D + sub * 16);
+            bt.sk[t] = load_f32<(FL & kNtScales) != 0>(sKp + r);
+            bt.sv[t] = load_f32<(FL & kNtScales) != 0>(sVp + r);
+        }
+        decode_math<D, NS, true>(bt.kv, bt.vv, bt.sk, bt.sv, row0, j1, q, qscale_l, m, l, acc);
     }
-    emit_row<D>(o, L, lane, bh, out, qout, qscale);
+    merge_block<D, MAXW>(m, l, acc, lane, grp, sub, w, nw, bh, s_ml, s_acc, out, qout, qscale);
 }
 
 // Paged variant of pass 1.  Unit = (b, h, split) as above, over positions
@@ -828,8 +925,34 @@ int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, con
     const float qk = (1.0f / std::sqrt((float)D)) * kLog2e;
     const dim3 grid((unsigned)ceil_div(units, kWavesPerBlock));
     constexpr int NS = D == 128 ? 8 : 4;
-    const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
     const bool vec = aligned_to(sKp, 16) && aligned_to(sVp, 16);
+    // page ids the chunks can reach, staged in LDS by the one-launch kernel
+    const long long n_tab = std::min<long long>(
+        max_pages, ceil_div((long long)plan.nsplit * plan.chunk, 1LL << log2_page));
+    if (plan.nsplit <= 8 && use_block_kernel() && n_tab * 4 <= kPagedLdsTableBytes) {
+        const int st = tuning_for(D).stagger;
+        const size_t lds = (size_t)n_tab * 4;
+#define INT8K_PAGED_BLOCK(FLV)                                                                 \
+    if (vec)                                                                                   \
+        decode_paged_block_kernel<D, NS, true, FLV, 8>                                         \
+            <<<(unsigned)BH, 64 * plan.nsplit, lds, stream>>>(                                 \
+                Q, Kp, Vp, sQ, sKp, sVp, tables, lens, out, o.q, o.qs, H, num_pages, log2_page, \
+                max_pages, (int)n_tab, plan.chunk, qk, st);                                     \
+    else                                                                                       \
+        decode_paged_block_kernel<D, NS, false, FLV, 8>                                        \
+            <<<(unsigned)BH, 64 * plan.nsplit, lds, stream>>>(                                 \
+                Q, Kp, Vp, sQ, sKp, sVp, tables, lens, out, o.q, o.qs, H, num_pages, log2_page, \
+                max_pages, (int)n_tab, plan.chunk, qk, st)
+        switch (tuning_for(D).flags & 3) {
+            case 0: INT8K_PAGED_BLOCK(0); break;
+            case 1: INT8K_PAGED_BLOCK(1); break;
+            case 2: INT8K_PAGED_BLOCK(2); break;
+            default: INT8K_PAGED_BLOCK(3); break;
+        }
+#undef INT8K_PAGED_BLOCK
+        return check_launch("decode_paged_block_kernel");
+    }
+    const bool final_pass = plan.nsplit == 1 && out != nullptr && aligned_to(out, 16);
 #define INT8K_PAGED_LAUNCH(FIN, FLV)                                                         \
     if (vec) decode_paged_kernel<D, NS, FIN, FLV, true><<<grid, kBlockThreads, 0, stream>>>( \
         Q, Kp, Vp, sQ, sKp, sVp, tables, lens, w.part_ml, w.part_acc, out, H, num_pages,     \

@@ -60,6 +60,21 @@ def test_paged_decode_forced_splits(gpu, nsplit):
     assert_attn_close(out.float().cpu().numpy(), _oracle(c))
 
 
+@pytest.mark.parametrize("L", [190000, 196900])
+def test_paged_decode_long_page_table(gpu, L):
+    # up to 8 chunks per (b,h) run as one launch with the page ids staged in LDS
+    # (11875 ids at L = 190000); a table past what LDS holds (12288 ids) runs the
+    # split + combine pair instead (12307 ids at L = 196900)
+    nsplit = 8
+    lens = [L, 4000]
+    c = workloads.paged_case(2, 1, 64, 16, lens, seed=11, device=gpu)
+    out = capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                      c["sK_pages"], c["sV_pages"], c["block_tables"],
+                                      c["context_lens"], c["max_context"], nsplit=nsplit)
+    torch.cuda.synchronize()
+    assert_attn_close(out.float().cpu().numpy(), _oracle(c))
+
+
 def test_paged_equals_contiguous_kernel(gpu):
     # identity page tables over a contiguous cache: same positions, same math
     B, H, D, S, P = 2, 4, 128, 640, 64
