@@ -370,11 +370,26 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     prefetch_tile<D, PAD>(pa, src, 0);
 
     // E: the exponent that keeps the scaled V^T in fp16 range, from max |sV| over
-    // the keys this block reads (a block-wide reduction through LDS).
+    // the keys this block reads (a block-wide reduction through LDS).  Each thread
+    // reads 16-byte vectors, kSvU of them in flight per round; dwords past kv_end
+    // read as zero (the buffer range is checked per dword).
     __shared__ float s_svmax[Shape<D>::kWaves];
     {
+        typedef float v4f __attribute__((ext_vector_type(4)));
+        constexpr int kT = Shape<D>::kThreads, kSvU = 4;
+        const __amdgpu_buffer_rsrc_t svr = make_buffer(sVbh, (uint32_t)kv_end * 4);
         float a = 0.f;
-        for (int j = threadIdx.x; j < kv_end; j += Shape<D>::kThreads) a = fmaxf(a, fabsf(sVbh[j]));
+        for (int j0 = 0; j0 < kv_end; j0 += 4 * kT * kSvU) {
+            v4f v[kSvU];
+#pragma unroll
+            for (int u = 0; u < kSvU; ++u)
+                v[u] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   svr, 4 * (j0 + 4 * (u * kT + (int)threadIdx.x)), 0, 0));
+#pragma unroll
+            for (int u = 0; u < kSvU; ++u)
+                a = fmaxf(a, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)),
+                                   fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+        }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) a = fmaxf(a, __shfl_xor(a, off));
         if (lane == 0) s_svmax[wave] = a;
