@@ -13,7 +13,8 @@ The default run (`--workload all`) measures every BASELINE configuration:
     line's `value`;
   * under `configs`: config 1 (B1 H12 D64 ctx 1K), config 3 (B8 H32 D64 ctx
     32K) with its ctx sweep 2K..16K, config 4 (the INT8 MLP, T=4096
-    4096->16384->4096) and config 5 (causal prefill B4 H32 S4096 D128).
+    4096->16384->4096), config 5 (causal prefill B4 H32 S4096 D128) and the
+    end-to-end pre-LN block, INT8 against FP16 (block.py).
 Every figure is the median of 5 windows of `--steps` steps after `--warmup`
 untimed steps, timed with HIP events on the launch stream; every config has
 its own `roofline` and an oracle parity check (all rows for decode).
@@ -753,12 +754,16 @@ def bench_all(args):
     torch.cuda.empty_cache()
     cfg5 = measure_prefill(args, dev, stream, None if args.no_cpu_baseline else 5.0,
                            extras=False)
+    torch.cuda.empty_cache()
+    blk = bench_block(args)
     res["configs"] = {
         "cfg1_decode_b1h12d64_s1024": cfg1,
         "cfg3_decode_b8h32d64_s32768": sweep[-1],
         "cfg3_ctx_sweep_b8h32d64": sweep[:-1],
         "cfg4_mlp_t4096_d4096_f16384": cfg4,
         "cfg5_prefill_causal_b4h32s4096d128": cfg5,
+        "block_d1024_h16_dff4096": {"metric": blk["metric"], "value": blk["value"],
+                                    "unit": blk["unit"], "rows": blk["config"]["rows"]},
     }
     return res
 
