@@ -14,10 +14,11 @@
 // V^T) and both key-scale vectors of a tile are staged in double-buffered LDS
 // by buffer loads: the next tile's loads are in flight in registers while the
 // current tile is computed, and there is one barrier per tile.  Causal grids
-// at head_dim <= 128 keep two tiles in flight (a second register set): all
-// heads are live at once there, so K/V come from beyond L2 and one step does
-// not cover the load latency.  The LDS reads of the MFMA fragments and key
-// scales are scheduled ahead of their uses.  Everything is
+// at head_dim <= 128 walk steps of two tiles over four LDS stages with two
+// register sets, so each load has a whole two-tile step to land (all heads
+// are live at once there, and K/V come from beyond L2), with one barrier per
+// step.  The LDS reads of the MFMA fragments and key scales are scheduled
+// ahead of their uses.  Everything is
 // computed transposed so that each lane owns one query:
 //   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows
 //                                   from LDS, B = Q kept in VGPRs)
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     extern __shared__ __align__(16) char smem[];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
     // Under the causal mask a query tile's work grows with its index, so the
     // grid is query-tile-major, heaviest tiles of every (b,h) first.  Without
@@ -361,13 +362,15 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int q_wave_last = min(qw0 + 31, S - 1);
 
     // Causal grids at D <= 128 keep two register sets of tiles in flight (their
-    // K/V come from further away: every head is live at once); the others one.
+    // K/V come from further away: every head is live at once) and stage four
+    // tiles in LDS; the others one set and two stages.
     constexpr int kDepth = (CAUSAL && D <= 128) ? 2 : 1;
     // The first tiles' loads go out before the exponent's reduction, so their
     // latency overlaps it.
     const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
     Prefetch<D> pa, pb;
     prefetch_tile<D, PAD>(pa, src, 0);
+    if constexpr (kDepth == 2) prefetch_tile<D, PAD>(pb, src, kKV);
 
     // E: the exponent that keeps the scaled V^T in fp16 range, from max |sV| over
     // the keys this block reads (a block-wide reduction through LDS).  Each thread
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const float vscale = __builtin_ldexpf(1.f, -vexp);  // V^T = fp16(v * sV * 2^-E)
     const float pexp = (float)vexp;                      // P = fp16(p * 2^E)
 
-    auto stage_of = [&](int kt) { return smem + (kt & 1) * St::kBytes; };
+    auto stage_of = [&](int kt) { return smem + (kt & (2 * kDepth - 1)) * St::kBytes; };
     // S^T = K . Q^T for the two 32-key halves of tile kt
     auto qk = [&](int kt, v16i (&sacc)[2]) {
         const char* st = stage_of(kt);
@@ -550,41 +553,77 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     };
 
     if constexpr (kDepth == 2) {
-        // Tile kt is computed from LDS stage kt&1.  Two register sets alternate:
-        // during step kt, set kt&1 holds tile kt+1 (loaded two steps earlier) and
-        // the other set tile kt+2.  At the end of the step the set is written to
-        // the other stage and refilled with tile kt+3; one barrier per step.
-        commit_tile<D>(pa, smem, vscale);
-        if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, kKV);
-        if (n_kv > 2) prefetch_tile<D, PAD>(pb, src, 2 * kKV);
+        // Steps of two tiles (kt even, kt+1): tile kt is computed from LDS stage
+        // kt&3.  At the start of a step the two register sets, loaded a whole
+        // step earlier, are written to the stages of tiles kt+2, kt+3 (the ones
+        // the previous step read, done before its barrier) and refilled with
+        // tiles kt+4, kt+5; one barrier per step makes them visible.  Writing the
+        // sets before the step's branches, and running the fast steps as an
+        // inner loop that the slow path leaves and re-enters with one update of
+        // O per step, keeps the compiler from copying O or the sets between
+        // registers on the fast path.  Loads past the block's last tile read
+        // in-bounds rows or zeros and are never computed.
+        commit_tile<D>(pa, stage_of(0), vscale);
+        commit_tile<D>(pb, stage_of(1), vscale);
+        prefetch_tile<D, PAD>(pa, src, 2 * kKV);
+        prefetch_tile<D, PAD>(pb, src, 3 * kKV);
         __syncthreads();
-        auto tile = [&](int kt) {
+        auto stage_next = [&](int kt) {
+            commit_tile<D>(pa, stage_of(kt + 2), vscale);
+            commit_tile<D>(pb, stage_of(kt + 3), vscale);
+            prefetch_tile<D, PAD>(pa, src, (kt + 4) * kKV);
+            prefetch_tile<D, PAD>(pb, src, (kt + 5) * kKV);
+        };
+        // A step on the fast path: both tiles' P from the current m, then both PV
+        // products.  False (nothing updated) when a tile of the step needs the
+        // slow path; the slow path then takes both.
+        auto fast_step = [&](int kt) {
+            if (!(full_tile(kt + 1) && qpos)) return false;
+            v16i sacc[2];
+            v8h pa_fr[4], pb_fr[4];
+            qk(kt, sacc);
+            const float ta = softmax_fast(kt, sacc, pa_fr);
+            schedule_qk();
+            qk(kt + 1, sacc);
+            const float tb = softmax_fast(kt + 1, sacc, pb_fr);
+            schedule_qk();
+            if (__ballot(!(ta <= 65504.f) | !(tb <= 65504.f))) return false;
+            lsum += ta + tb;
+            pv(kt, pa_fr);
+            schedule_pv();
+            pv(kt + 1, pb_fr);
+            schedule_pv();
+            return true;
+        };
+        auto slow_tile = [&](int kt) {
             v16i sacc[2];
             v8h pfr[4];
-            if (full_tile(kt) && qpos) {
-                qk(kt, sacc);
-                const float tsum = softmax_fast(kt, sacc, pfr);
-                schedule_qk();
-                if (__ballot(!(tsum <= 65504.f))) softmax_slow(kt, sacc, pfr);
-                else lsum += tsum;
-            } else {
-                qk(kt, sacc);
-                softmax_slow(kt, sacc, pfr);
-            }
+            qk(kt, sacc);
+            softmax_slow(kt, sacc, pfr);
             pv(kt, pfr);
-            schedule_pv();
         };
-        auto step = [&](int kt, Prefetch<D>& pfx) {
-            if (computes(kt)) tile(kt);
-            if (kt + 1 < n_kv) {
-                commit_tile<D>(pfx, smem + ((kt + 1) & 1) * St::kBytes, vscale);
-                if (kt + 3 < n_kv) prefetch_tile<D, PAD>(pfx, src, (kt + 3) * kKV);
+        // The wave computes tiles [0, n_comp); the causal mask hides later ones from all its queries.
+        const int n_comp = CAUSAL ? min(n_kv, q_wave_last / kKV + 1) : n_kv;
+        int kt = 0;  // first tile of a step
+        while (kt < n_comp) {
+            bool slow = false;
+            for (; kt < n_comp; kt += 2) {
+                stage_next(kt);
+                if (kt + 1 >= n_comp || !fast_step(kt)) {
+                    slow = true;
+                    break;
+                }
+                __syncthreads();
             }
+            if (!slow) break;
+            slow_tile(kt);
+            if (kt + 1 < n_comp) slow_tile(kt + 1);
             __syncthreads();
-        };
-        for (int kt = 0; kt < n_kv; kt += 2) {
-            step(kt, pa);
-            if (kt + 1 < n_kv) step(kt + 1, pb);
+            kt += 2;
+        }
+        for (; kt < n_kv; kt += 2) {
+            stage_next(kt);
+            __syncthreads();
         }
     } else {
         // Tile kt is computed from LDS stage kt&1.  The register set holds tile
@@ -942,9 +981,11 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
     const int n_qtiles = (S + kQ - 1) / kQ;
     const long long blocks = (long long)BH * n_qtiles;
     const float qk = (1.0f / std::sqrt((float)dm)) * kLog2e;
-    const int lds = 2 * Stage<D>::kBytes;
+    // causal grids at D <= 128 stage four tiles (see prefill_kernel's kDepth)
+    const int lds_max = (D <= 128 ? 4 : 2) * Stage<D>::kBytes;
+    const int lds = (causal && D <= 128 ? 4 : 2) * Stage<D>::kBytes;
     static PerDeviceOnce lds_once;
-    const int st = set_lds_limit(lds_once, lds, prefill_kernel<D, true, false>,
+    const int st = set_lds_limit(lds_once, lds_max, prefill_kernel<D, true, false>,
                                  prefill_kernel<D, false, false>, prefill_kernel<D, true, true>,
                                  prefill_kernel<D, false, true>);
     if (st != INT8K_OK) return st;
