@@ -13,12 +13,11 @@
 // and walks the KV sequence in tiles of 64 keys.  K (int8 rows), V (as fp16
 // V^T) and both key-scale vectors of a tile are staged in double-buffered LDS
 // by buffer loads: the next tile's loads are in flight in registers while the
-// current tile is computed, and there is one barrier per tile.  Causal grids
-// at head_dim <= 128 walk steps of two tiles over four LDS stages with two
-// register sets, so each load has a whole two-tile step to land (all heads
-// are live at once there, and K/V come from beyond L2), with one barrier per
-// step.  The LDS reads of the MFMA fragments and key scales are scheduled
-// ahead of their uses.  Everything is
+// current tile is computed, and there is one barrier per tile.  The LDS reads
+// of the MFMA fragments and key scales are scheduled ahead of their uses.  The
+// wave index is read into a scalar register, so every per-wave condition of the
+// tile loop (causal skip, masked tile, fast or slow path) is a scalar branch.
+// Everything is
 // computed transposed so that each lane owns one query:
 //   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows
 //                                   from LDS, B = Q kept in VGPRs)
@@ -361,16 +360,11 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int n_kv = (kv_end + kKV - 1) / kKV;
     const int q_wave_last = min(qw0 + 31, S - 1);
 
-    // Causal grids at D <= 128 keep two register sets of tiles in flight (their
-    // K/V come from further away: every head is live at once) and stage four
-    // tiles in LDS; the others one set and two stages.
-    constexpr int kDepth = (CAUSAL && D <= 128) ? 2 : 1;
-    // The first tiles' loads go out before the exponent's reduction, so their
+    // The first tile's loads go out before the exponent's reduction, so their
     // latency overlaps it.
     const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
-    Prefetch<D> pa, pb;
+    Prefetch<D> pa;
     prefetch_tile<D, PAD>(pa, src, 0);
-    if constexpr (kDepth == 2) prefetch_tile<D, PAD>(pb, src, kKV);
 
     // E: the exponent that keeps the scaled V^T in fp16 range, from max |sV| over
     // the keys this block reads (a block-wide reduction through LDS).  Each thread
@@ -413,7 +407,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const float vscale = __builtin_ldexpf(1.f, -vexp);  // V^T = fp16(v * sV * 2^-E)
     const float pexp = (float)vexp;                      // P = fp16(p * 2^E)
 
-    auto stage_of = [&](int kt) { return smem + (kt & (2 * kDepth - 1)) * St::kBytes; };
+    auto stage_of = [&](int kt) { return smem + (kt & 1) * St::kBytes; };
     // S^T = K . Q^T for the two 32-key halves of tile kt
     auto qk = [&](int kt, v16i (&sacc)[2]) {
         const char* st = stage_of(kt);
@@ -448,11 +442,6 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     };
     // A wave computes tile kt unless the causal mask hides all of it from the wave's queries.
     auto computes = [&](int kt) { return !(CAUSAL && kt * kKV > q_wave_last); };
-    // Tile kt has no key masked for any query of the wave.
-    auto full_tile = [&](int kt) {
-        const int k0 = kt * kKV;
-        return k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
-    };
     // Keep the K-fragment and sK reads of the fast tile ahead of their uses
     // (the compiler otherwise waits on each LDS read right before its MFMA).
     auto schedule_qk = [&]() {
@@ -493,202 +482,40 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     // tile, masked edge and diagonal tiles, a sum past the fp16 range) takes the slow
     // path, which sets m to the exact running max and rescales O and l.  l sums the
     // fp16 P that enter the PV product.
-    auto softmax_fast = [&](int kt, const v16i (&sacc)[2], v8h (&pfr)[4]) {
-        const float* sk_l = sk_of(kt);
-        const float shift = pexp - m;
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
-                const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
-                    pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
-                        (_Float16)fast_exp2(fmaf(u, qscale, shift));
-                }
-            }
-        return psum(pfr);
-    };
-    auto softmax_slow = [&](int kt, const v16i (&sacc)[2], v8h (&pfr)[4]) {
-        const int k0 = kt * kKV;
-        const float* sk_l = sk_of(kt);
-        float sc[2][16];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
-                const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int key = k0 + 32 * T + 8 * g + 4 * h + c;
-                    const bool masked = (key >= S) | (CAUSAL & (key > q));
-                    const float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
-                    sc[T][4 * g + c] = masked ? -INFINITY : v;
-                    mx = fmaxf(mx, sc[T][4 * g + c]);
-                }
-            }
-        mx = max_xor32(mx);
-        const float m_new = fmaxf(m, mx);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float corr = fast_exp2(m - m_use);
-#pragma unroll
-        for (int t = 0; t < NS; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-        m = m_new;
-        const float shift = pexp - m_use;
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
-                        (_Float16)fast_exp2(sc[T][4 * g + c] + shift);
-        lsum = lsum * corr + psum(pfr);
-    };
-
-    if constexpr (kDepth == 2) {
-        // Steps of two tiles (kt even, kt+1): tile kt is computed from LDS stage
-        // kt&3.  At the start of a step the two register sets, loaded a whole
-        // step earlier, are written to the stages of tiles kt+2, kt+3 (the ones
-        // the previous step read, done before its barrier) and refilled with
-        // tiles kt+4, kt+5; one barrier per step makes them visible.  Writing the
-        // sets before the step's branches, and running the fast steps as an
-        // inner loop that the slow path leaves and re-enters with one update of
-        // O per step, keeps the compiler from copying O or the sets between
-        // registers on the fast path.  Loads past the block's last tile read
-        // in-bounds rows or zeros and are never computed.
-        commit_tile<D>(pa, stage_of(0), vscale);
-        commit_tile<D>(pb, stage_of(1), vscale);
-        prefetch_tile<D, PAD>(pa, src, 2 * kKV);
-        prefetch_tile<D, PAD>(pb, src, 3 * kKV);
+    //
+    // Tile kt is computed from LDS stage kt&1.  The register set holds tile
+    // kt+1 while tile kt is computed; at the end of the step it is written to
+    // the other stage, refilled with tile kt+2, and the step's one barrier
+    // follows.  The fast path runs as an inner loop that the slow path leaves
+    // and re-enters, so O has no conditional update inside it.
+    commit_tile<D>(pa, smem, vscale);
+    if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, kKV);
+    __syncthreads();
+    auto advance = [&](int kt) {
+        if (kt + 1 < n_kv) {
+            commit_tile<D>(pa, smem + ((kt + 1) & 1) * St::kBytes, vscale);
+            if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pa, src, (kt + 2) * kKV);
+        }
+        // tile kt+1 is in LDS and every wave is done reading stage kt&1
         __syncthreads();
-        auto stage_next = [&](int kt) {
-            commit_tile<D>(pa, stage_of(kt + 2), vscale);
-            commit_tile<D>(pb, stage_of(kt + 3), vscale);
-            prefetch_tile<D, PAD>(pa, src, (kt + 4) * kKV);
-            prefetch_tile<D, PAD>(pb, src, (kt + 5) * kKV);
-        };
-        // A step on the fast path: both tiles' P from the current m, then both PV
-        // products.  False (nothing updated) when a tile of the step needs the
-        // slow path; the slow path then takes both.
-        auto fast_step = [&](int kt) {
-            if (!(full_tile(kt + 1) && qpos)) return false;
-            v16i sacc[2];
-            v8h pa_fr[4], pb_fr[4];
-            qk(kt, sacc);
-            const float ta = softmax_fast(kt, sacc, pa_fr);
-            schedule_qk();
-            qk(kt + 1, sacc);
-            const float tb = softmax_fast(kt + 1, sacc, pb_fr);
-            schedule_qk();
-            if (__ballot(!(ta <= 65504.f) | !(tb <= 65504.f))) return false;
-            lsum += ta + tb;
-            pv(kt, pa_fr);
-            schedule_pv();
-            pv(kt + 1, pb_fr);
-            schedule_pv();
-            return true;
-        };
-        auto slow_tile = [&](int kt) {
-            v16i sacc[2];
-            v8h pfr[4];
-            qk(kt, sacc);
-            softmax_slow(kt, sacc, pfr);
-            pv(kt, pfr);
-        };
-        // The wave computes tiles [0, n_comp); the causal mask hides later ones from all its queries.
-        const int n_comp = CAUSAL ? min(n_kv, q_wave_last / kKV + 1) : n_kv;
-        int kt = 0;  // first tile of a step
-        while (kt < n_comp) {
-            bool slow = false;
-            for (; kt < n_comp; kt += 2) {
-                stage_next(kt);
-                if (kt + 1 >= n_comp || !fast_step(kt)) {
+    };
+    int kt = 0;
+    while (kt < n_kv) {
+        v16i sacc[2];
+        bool slow = false;
+        for (; kt < n_kv; ++kt) {
+            if (computes(kt)) {
+                const int k0 = kt * kKV;
+                const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
+                if (!(full && qpos)) {
+                    qk(kt, sacc);
                     slow = true;
                     break;
                 }
-                __syncthreads();
-            }
-            if (!slow) break;
-            slow_tile(kt);
-            if (kt + 1 < n_comp) slow_tile(kt + 1);
-            __syncthreads();
-            kt += 2;
-        }
-        for (; kt < n_kv; kt += 2) {
-            stage_next(kt);
-            __syncthreads();
-        }
-    } else {
-        // Tile kt is computed from LDS stage kt&1.  The register set holds tile
-        // kt+1 while tile kt is computed; at the end of the step it is written to
-        // the other stage, refilled with tile kt+2, and the step's one barrier
-        // follows.  The fast path runs as an inner loop that the slow path leaves
-        // and re-enters, so O has no conditional update inside it.
-        commit_tile<D>(pa, smem, vscale);
-        if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, kKV);
-        __syncthreads();
-        auto advance = [&](int kt) {
-            if (kt + 1 < n_kv) {
-                commit_tile<D>(pa, smem + ((kt + 1) & 1) * St::kBytes, vscale);
-                if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pa, src, (kt + 2) * kKV);
-            }
-            // tile kt+1 is in LDS and every wave is done reading stage kt&1
-            __syncthreads();
-        };
-        int kt = 0;
-        while (kt < n_kv) {
-            v16i sacc[2];
-            bool slow = false;
-            for (; kt < n_kv; ++kt) {
-                if (computes(kt)) {
-                    const int k0 = kt * kKV;
-                    const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
-                    if (!(full && qpos)) {
-                        qk(kt, sacc);
-                        slow = true;
-                        break;
-                    }
-                    qk(kt, sacc);
-                    const float* sk_l = sk_of(kt);
-                    const float shift = pexp - m;
-                    v8h pfr[4];
-#pragma unroll
-                    for (int T = 0; T < 2; ++T)
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
-                            const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
-#pragma unroll
-                            for (int c = 0; c < 4; ++c) {
-                                const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
-                                pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
-                                    (_Float16)fast_exp2(fmaf(u, qscale, shift));
-                            }
-                        }
-                    schedule_qk();
-                    const float tsum = psum(pfr);
-                    if (__ballot(!(tsum <= 65504.f))) { slow = true; break; }
-                    lsum += tsum;
-                    pv(kt, pfr);
-                    schedule_pv();
-                }
-                advance(kt);
-            }
-            if (!slow) break;
-            // Slow path for tile kt (its S^T is in sacc): s = acc * qscale * sK with masked
-            // keys at -inf, exact running max, rescale of O and l.
-            {
-                const int k0 = kt * kKV;
+                qk(kt, sacc);
                 const float* sk_l = sk_of(kt);
-                float sc[2][16];
-                float mx = -INFINITY;
+                const float shift = pexp - m;
+                v8h pfr[4];
 #pragma unroll
                 for (int T = 0; T < 2; ++T)
 #pragma unroll
@@ -697,39 +524,68 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                         const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
-                            float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
-                            const int key = k0 + 32 * T + 8 * g + 4 * h + c;
-                            if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
-                            sc[T][4 * g + c] = v;
-                            mx = fmaxf(mx, v);
+                            const float u = static_cast<float>(sacc[T][4 * g + c]) * skk[c];
+                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
+                                (_Float16)fast_exp2(fmaf(u, qscale, shift));
                         }
                     }
-                mx = max_xor32(mx);
-                const float m_new = fmaxf(m, mx);
-                const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-                const float corr = fast_exp2(m - m_use);
-                lsum *= corr;
-#pragma unroll
-                for (int t = 0; t < NS; ++t)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-                m = m_new;
-                const float shift = pexp - m_use;
-                v8h pfr[4];
-#pragma unroll
-                for (int T = 0; T < 2; ++T)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
-                                (_Float16)fast_exp2(sc[T][4 * g + c] + shift);
-                lsum += psum(pfr);
+                schedule_qk();
+                const float tsum = psum(pfr);
+                if (__ballot(!(tsum <= 65504.f))) { slow = true; break; }
+                lsum += tsum;
                 pv(kt, pfr);
+                schedule_pv();
             }
             advance(kt);
-            ++kt;
         }
+        if (!slow) break;
+        // Slow path for tile kt (its S^T is in sacc): s = acc * qscale * sK with masked
+        // keys at -inf, exact running max, rescale of O and l.
+        {
+            const int k0 = kt * kKV;
+            const float* sk_l = sk_of(kt);
+            float sc[2][16];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 skv = *reinterpret_cast<const float4*>(sk_l + 32 * T + 8 * g + 4 * h);
+                    const float skk[4] = {skv.x, skv.y, skv.z, skv.w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        float v = static_cast<float>(sacc[T][4 * g + c]) * qscale * skk[c];
+                        const int key = k0 + 32 * T + 8 * g + 4 * h + c;
+                        if (key >= S || (CAUSAL && key > q)) v = -INFINITY;
+                        sc[T][4 * g + c] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                }
+            mx = max_xor32(mx);
+            const float m_new = fmaxf(m, mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float corr = fast_exp2(m - m_use);
+            lsum *= corr;
+#pragma unroll
+            for (int t = 0; t < NS; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+            m = m_new;
+            const float shift = pexp - m_use;
+            v8h pfr[4];
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        pfr[2 * T + (g >> 1)][4 * (g & 1) + c] =
+                            (_Float16)fast_exp2(sc[T][4 * g + c] + shift);
+            lsum += psum(pfr);
+            pv(kt, pfr);
+        }
+        advance(kt);
+        ++kt;
     }
 
     const float L = sum_xor32(lsum);
@@ -981,11 +837,9 @@ int launch_prefill(const int8_t* Q, const int8_t* K, const int8_t* V, uint16_t* 
     const int n_qtiles = (S + kQ - 1) / kQ;
     const long long blocks = (long long)BH * n_qtiles;
     const float qk = (1.0f / std::sqrt((float)dm)) * kLog2e;
-    // causal grids at D <= 128 stage four tiles (see prefill_kernel's kDepth)
-    const int lds_max = (D <= 128 ? 4 : 2) * Stage<D>::kBytes;
-    const int lds = (causal && D <= 128 ? 4 : 2) * Stage<D>::kBytes;
+    const int lds = 2 * Stage<D>::kBytes;
     static PerDeviceOnce lds_once;
-    const int st = set_lds_limit(lds_once, lds_max, prefill_kernel<D, true, false>,
+    const int st = set_lds_limit(lds_once, lds, prefill_kernel<D, true, false>,
                                  prefill_kernel<D, false, false>, prefill_kernel<D, true, true>,
                                  prefill_kernel<D, false, true>);
     if (st != INT8K_OK) return st;
