@@ -345,8 +345,9 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
         qf[s] = (!PAD || 32 * s + 16 * h < dm)
                     ? *reinterpret_cast<const v4i*>(Qbh + (size_t)min(q, S - 1) * dm + 32 * s + 16 * h)
                     : v4i{0, 0, 0, 0};
-    const float qscale = qok ? sQ[base + q] * qk_scale_log2 : 0.f;
-    const bool qpos = __ballot(!(qscale >= 0.f)) == 0;  // wave-uniform
+    // The query scale is loaded here but first used after the V-scale exponent's
+    // reduction, so its wait joins the first tile's instead of adding a latency.
+    const float sq_raw = qok ? sQ[base + q] : 0.f;
 
     v16f o[NS];
 #pragma unroll
@@ -387,8 +388,19 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                 a = fmaxf(a, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)),
                                    fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
         }
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) a = fmaxf(a, __shfl_xor(a, off));
+        // max over the wave on the VALU: DPP inside each 16-lane row, then the
+        // row and half swaps (no LDS round trips)
+        auto dmax = [](float x, int y) { return fmaxf(x, __int_as_float(y)); };
+        a = dmax(a, dpp_xor1(__float_as_int(a)));
+        a = dmax(a, dpp_xor2(__float_as_int(a)));
+        a = dmax(a, dpp_half_mirror(__float_as_int(a)));
+        a = dmax(a, dpp_row_mirror(__float_as_int(a)));
+        {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(a), __float_as_int(a),
+                                                            false, false);
+            a = fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+        }
+        a = max_xor32(a);
         if (lane == 0) s_svmax[wave] = a;
     }
     __syncthreads();
@@ -406,6 +418,8 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     }
     const float vscale = __builtin_ldexpf(1.f, -vexp);  // V^T = fp16(v * sV * 2^-E)
     const float pexp = (float)vexp;                      // P = fp16(p * 2^E)
+    const float qscale = sq_raw * qk_scale_log2;
+    const bool qpos = __ballot(!(qscale >= 0.f)) == 0;  // wave-uniform
 
     auto stage_of = [&](int kt) { return smem + (kt & 1) * St::kBytes; };
     // S^T = K . Q^T for the two 32-key halves of tile kt
