@@ -478,8 +478,11 @@ def bench_decode_paged(args):
     log(f"[bench] parity sample (sequences {rows}): max_abs={err:.2e}")
     if not (err <= 2e-2):
         raise SystemExit(f"paged decode output does not match the oracle (max_abs={err})")
+    nsplit = capi.decode_paged_num_splits(B, H, S, D, args.nsplit)
+    one_launch = (nsplit <= 8 and npp * 4 <= (48 << 10)
+                  and os.environ.get("INT8K_DECODE_BLOCK", "1") != "0")
     return {
-        "metric": "paged decode attn effective KV-read TB/s, B=32 H=32 D=128 8K ctx",
+        "metric": f"paged decode attn effective KV-read TB/s, B={B} H={H} D={D} ctx={S}",
         "value": round(achieved_gbs / 1e3, 4), "unit": "TB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8",
@@ -488,8 +491,9 @@ def bench_decode_paged(args):
                    "pages": NP},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "decode_paged_kernel + decode_combine_kernel (one step)"},
+                     "traffic": None, "nsplit": nsplit,
+                     "kernel": ("decode_paged_block_kernel (one launch per step)" if one_launch
+                                else "decode_paged_kernel + decode_combine_kernel (one step)")},
         "cpu_baseline": None,
     }
 

@@ -147,6 +147,12 @@ int int8k_decode_attention_forward_cache_quant(
 size_t int8k_decode_attention_paged_workspace_bytes(int B, int H, int max_context,
                                                     int head_dim, int nsplit);
 
+/* Chunks per (b, h) the paged call plans for these arguments (0 if they are
+ * invalid).  Plans of up to 8 chunks whose page-id table fits 48 KiB run as
+ * one launch; larger ones as a split kernel plus a combine kernel. */
+int int8k_decode_attention_paged_num_splits(int B, int H, int max_context, int head_dim,
+                                            int nsplit);
+
 int int8k_decode_attention_forward_paged(
     const int8_t* Q, const int8_t* K_pages, const int8_t* V_pages, uint16_t* out,
     const float* scale_Q, const float* sK_pages, const float* sV_pages,

@@ -17,6 +17,13 @@
 //    iteration covers R = G*NSLOT rows: group g owns rows g*NSLOT .. +NSLOT-1
 //    of the block, one per load slot, so every slot of every lane is an
 //    immediate offset from one base address.
+//  * Paired rows (D=64, 4 slots, the 8-wave one-launch kernels): a 64-byte
+//    row is half a 128-byte line, so groups 2h and 2h+1 take the even and the
+//    odd rows of block rows 8h..8h+7 (slot t: row 8h + o + 2t) and every load
+//    instruction covers whole lines.  That makes non-temporal K/V loads pay
+//    at D=64 too; with half lines per instruction they cost 20-100%.  Each
+//    lane then loads one of its group's four scales and the group reads them
+//    with a DPP quad broadcast.
 //  * QK: 4 v_dot4_i32_i8 per slot per lane (exact int32), then a DPP sum over
 //    the LPR lanes of the group (no LDS).  The group's lanes all hold the score.
 //  * Softmax: every row-group keeps its own online-softmax state (m, l) in the
@@ -58,12 +65,24 @@ struct DecodeGeom {
 // Rows per wave iteration for a head dim (host side).
 inline int rows_per_iter(int D, int ns) { return (64 / (D / 16)) * ns; }
 
+// Paired rows (the 8-wave one-launch kernels at D=64 with 4 slots): group
+// 2h+o owns rows 8h+o, +2, +4, +6 of a wave iteration's block, so each load
+// slot covers whole 128-byte lines; otherwise group g owns rows g*NS .. +NS-1.
+constexpr bool paired_rows(int D, int NS, int MAXW) { return D == 64 && NS == 4 && MAXW <= 8; }
+
+template <bool PAIRED, int NS>
+__device__ __forceinline__ int group_row0(int grp) {
+    if constexpr (PAIRED) return 8 * (grp >> 1) + (grp & 1);
+    else return grp * NS;
+}
+
 // Launch-time tuning of the decode kernel.
 struct DecodeTuning {
     int slots;         // NS
     int flags;         // kNtKV | kNtScales
     int target_units;  // units (waves) to aim for
     int stagger;       // rotate each unit's starting iteration
+    int pair_flags;    // load flags of the paired-row kernels (D=64, 4 slots, <= 8 chunks)
 };
 
 struct SplitPlan {
@@ -96,22 +115,26 @@ inline int env_int(const char* name, int dflt) {
 // Defaults measured on MI355X at the BASELINE shapes (B32 H32 D128 8K and
 // B8 H32 D64 2K..32K): D=128 — 8 slots, non-temporal K/V loads, ~8192 units
 // (two resident rounds at 16 waves/CU); D=64 — 4 slots, non-temporal scale
-// loads, ~2048 units (8 chunks per (b,h) at B8 H32: two waves per SIMD).
-// Both rotate each unit's starting iteration (stagger), which was worth 2-5%.
-// The INT8K_DECODE_* variables override these for tuning sweeps (read once
-// per process).
+// loads, ~2048 units (8 chunks per (b,h) at B8 H32: two waves per SIMD);
+// its paired-row kernels (plans of up to 8 chunks) load K/V non-temporally
+// and the scales as plain loads (ctx 2K-32K: 5-11% faster than the grouped
+// rows with non-temporal scales).  Both rotate each unit's starting
+// iteration (stagger), which was worth 2-5%.  The INT8K_DECODE_* variables
+// override these for tuning sweeps (read once per process).
 DecodeTuning tuning_for(int D) {
     static const int e_slots = env_int("INT8K_DECODE_SLOTS", 0);
     static const int e_flags = env_int("INT8K_DECODE_FLAGS", -1);
     static const int e_units = env_int("INT8K_DECODE_TARGET_UNITS", 0);
     static const int e_stagger = env_int("INT8K_DECODE_STAGGER", -1);
+    static const int e_pair = env_int("INT8K_DECODE_PAIR_FLAGS", -1);
     DecodeTuning t;
-    if (D == 128) t = DecodeTuning{8, kNtKV, 8192, 1};
-    else t = DecodeTuning{4, kNtScales, 2048, 1};
+    if (D == 128) t = DecodeTuning{8, kNtKV, 8192, 1, kNtKV};
+    else t = DecodeTuning{4, kNtScales, 2048, 1, kNtKV};
     if (e_slots == 4 || e_slots == 8) t.slots = e_slots;
     if (e_flags >= 0) t.flags = e_flags & 3;
     if (e_units > 0) t.target_units = e_units;
     if (e_stagger >= 0) t.stagger = e_stagger;
+    if (e_pair >= 0) t.pair_flags = e_pair & 3;
     return t;
 }
 
@@ -179,14 +202,29 @@ __device__ __forceinline__ int group_sum(int v) {
     else return group4_sum(v);
 }
 
+// Lane t's value of each 4-lane quad, in every lane of the quad (DPP
+// quad_perm [t,t,t,t]); t is a compile-time constant after unrolling.
+__device__ __forceinline__ float quad_bcast(float x, int t) {
+    const int v = __float_as_int(x);
+    switch (t) {
+        case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, false));
+        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, false));
+        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, false));
+        default: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, false));
+    }
+}
+
 // QK^T, online softmax and PV for one wave iteration whose NSLOT rows per
 // group are loaded (kv, vv, sk, sv).  MASKED: rows >= j1 get score -inf and
-// weight 0 (their loads point at some valid row).
-template <int D, int NS, bool MASKED>
+// weight 0 (their loads point at some valid row).  RS: rows between slots
+// (2 for paired rows).  QB: sk[0]/sv[0] hold the scale of the lane's own slot
+// (lane s of the 4-lane group: slot s), read by the group with quad_bcast.
+template <int D, int NS, bool MASKED, int RS = 1, bool QB = false>
 __device__ __forceinline__ void decode_math(const Int4 (&kv)[NS], const Int4 (&vv)[NS],
                                             const float (&sk)[NS], const float (&sv)[NS],
                                             int row0, int j1, const Int4& q, float qscale,
                                             float& m, float& l, float* acc) {
+    static_assert(!QB || (NS == 4 && D == 64), "quad broadcast: one scale per lane of a group");
     // QK^T: exact int32 dot per row, summed over the LPR lanes of the group.
     float sc[NS];
 #pragma unroll
@@ -196,9 +234,10 @@ __device__ __forceinline__ void decode_math(const Int4 (&kv)[NS], const Int4 (&v
         d = __builtin_amdgcn_sdot4(q.z, kv[t].z, d, false);
         d = __builtin_amdgcn_sdot4(q.w, kv[t].w, d, false);
         d = group_sum<D>(d);
-        sc[t] = static_cast<float>(d) * qscale * sk[t];
+        const float skt = QB ? quad_bcast(sk[0], t) : sk[t];
+        sc[t] = static_cast<float>(d) * qscale * skt;
         if constexpr (MASKED) {
-            if (row0 + t >= j1) sc[t] = -INFINITY;
+            if (row0 + t * RS >= j1) sc[t] = -INFINITY;
         }
     }
 
@@ -216,9 +255,9 @@ __device__ __forceinline__ void decode_math(const Int4 (&kv)[NS], const Int4 (&v
     for (int t = 0; t < NS; ++t) {
         const float p = fast_exp2(sc[t] - m_use);
         l += p;
-        float w = p * sv[t];
+        float w = p * (QB ? quad_bcast(sv[0], t) : sv[t]);
         if constexpr (MASKED) {
-            if (row0 + t >= j1) w = 0.f;
+            if (row0 + t * RS >= j1) w = 0.f;
         }
         fma_bytes(acc + 0, vv[t].x, w);
         fma_bytes(acc + 4, vv[t].y, w);
@@ -235,8 +274,10 @@ struct IterBuf {
     float sk[NS], sv[NS];
 };
 
-// The loads of an unmasked wave iteration whose group rows start at row0.
-template <int D, int NS, bool VEC_SCALES, int FL>
+// The loads of an unmasked wave iteration whose group rows start at row0 and
+// lie RS rows apart.  Paired rows with vector-capable scales (RS == 2 and
+// VEC_SCALES) load one scale per lane, slot `sub` (decode_math's QB).
+template <int D, int NS, bool VEC_SCALES, int FL, int RS = 1>
 __device__ __forceinline__ void load_iter(IterBuf<NS>& b, const int8_t* __restrict__ Kbh,
                                           const int8_t* __restrict__ Vbh,
                                           const float* __restrict__ sKbh,
@@ -244,10 +285,13 @@ __device__ __forceinline__ void load_iter(IterBuf<NS>& b, const int8_t* __restri
     const int8_t* kp = Kbh + (size_t)row0 * D + sub * 16;
     const int8_t* vp = Vbh + (size_t)row0 * D + sub * 16;
 #pragma unroll
-    for (int t = 0; t < NS; ++t) b.kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * D);
+    for (int t = 0; t < NS; ++t) b.kv[t] = load_kv16<(FL & kNtKV) != 0>(kp + t * RS * D);
 #pragma unroll
-    for (int t = 0; t < NS; ++t) b.vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * D);
-    if constexpr (VEC_SCALES) {
+    for (int t = 0; t < NS; ++t) b.vv[t] = load_kv16<(FL & kNtKV) != 0>(vp + t * RS * D);
+    if constexpr (VEC_SCALES && RS == 2) {
+        b.sk[0] = load_f32<(FL & kNtScales) != 0>(sKbh + row0 + 2 * sub);
+        b.sv[0] = load_f32<(FL & kNtScales) != 0>(sVbh + row0 + 2 * sub);
+    } else if constexpr (VEC_SCALES) {
 #pragma unroll
         for (int t = 0; t < NS; t += 4) {
             typedef float v4f __attribute__((ext_vector_type(4)));
@@ -265,16 +309,17 @@ __device__ __forceinline__ void load_iter(IterBuf<NS>& b, const int8_t* __restri
     } else {
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
-            b.sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + row0 + t);
-            b.sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + row0 + t);
+            b.sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + row0 + t * RS);
+            b.sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + row0 + t * RS);
         }
     }
 }
 
 // One wave iteration over NSLOT rows per group.  MASKED handles the last
 // partial block of a chunk: rows >= j1 get score -inf and weight 0 (their
-// loads are redirected to row j1-1, which is in bounds).
-template <int D, int NS, bool MASKED, bool VEC_SCALES, int FL>
+// loads are redirected to row j1-1, which is in bounds).  RS: rows between
+// slots (2 for paired rows).
+template <int D, int NS, bool MASKED, bool VEC_SCALES, int FL, int RS = 1>
 __device__ __forceinline__ void decode_iter(
     const int8_t* __restrict__ Kbh, const int8_t* __restrict__ Vbh,
     const float* __restrict__ sKbh, const float* __restrict__ sVbh,
@@ -282,18 +327,19 @@ __device__ __forceinline__ void decode_iter(
     float& m, float& l, float* acc) {
     IterBuf<NS> b;
     if constexpr (!MASKED) {
-        load_iter<D, NS, VEC_SCALES, FL>(b, Kbh, Vbh, sKbh, sVbh, row0, sub);
+        load_iter<D, NS, VEC_SCALES, FL, RS>(b, Kbh, Vbh, sKbh, sVbh, row0, sub);
     } else {
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
-            const int r = min(row0 + t, j1 - 1);
+            const int r = min(row0 + t * RS, j1 - 1);
             b.kv[t] = load_kv16<(FL & kNtKV) != 0>(Kbh + (size_t)r * D + sub * 16);
             b.vv[t] = load_kv16<(FL & kNtKV) != 0>(Vbh + (size_t)r * D + sub * 16);
             b.sk[t] = load_f32<(FL & kNtScales) != 0>(sKbh + r);
             b.sv[t] = load_f32<(FL & kNtScales) != 0>(sVbh + r);
         }
     }
-    decode_math<D, NS, MASKED>(b.kv, b.vv, b.sk, b.sv, row0, j1, q, qscale, m, l, acc);
+    decode_math<D, NS, MASKED, RS, (!MASKED && VEC_SCALES && RS == 2)>(
+        b.kv, b.vv, b.sk, b.sv, row0, j1, q, qscale, m, l, acc);
 }
 
 // Merges the G row-group states of a wave (lanes with equal `sub`) and writes
@@ -469,44 +515,51 @@ __global__ __launch_bounds__(kBlockThreads) void decode_combine_kernel(
 
 // The n_full whole iterations of a wave's chunk, starting at iteration `it` and
 // wrapping around.  roff(i): the row offset (from the K/V/scale bases) of the
-// group's first row in iteration i.  PIPE: two register sets, iteration
-// k+1's loads issued before iteration k is computed (the fences keep the
-// compiler from sinking them).
-template <int D, int NS, bool VEC_SCALES, int FL, bool PIPE, typename RowOff>
+// group's first row in iteration i; RS: rows between its slots.  PIPE: two
+// register sets, iteration k+1's loads issued before iteration k is computed
+// (the fences keep the compiler from sinking them).
+template <int D, int NS, bool VEC_SCALES, int FL, bool PIPE, int RS, typename RowOff>
 __device__ __forceinline__ void walk_iters(const int8_t* __restrict__ K,
                                            const int8_t* __restrict__ V,
                                            const float* __restrict__ sK,
                                            const float* __restrict__ sV, RowOff roff, int n_full,
                                            int it, int sub, const Int4& q, float qscale, float& m,
                                            float& l, float* acc) {
+    constexpr bool QB = VEC_SCALES && RS == 2;
     auto nxt = [&](int i) { return (i + 1 == n_full) ? 0 : i + 1; };
+    auto load = [&](IterBuf<NS>& b, int i) {
+        load_iter<D, NS, VEC_SCALES, FL, RS>(b, K, V, sK, sV, roff(i), sub);
+    };
+    auto math = [&](const IterBuf<NS>& b) {
+        decode_math<D, NS, false, RS, QB>(b.kv, b.vv, b.sk, b.sv, 0, 0, q, qscale, m, l, acc);
+    };
     if constexpr (PIPE) {
         IterBuf<NS> ba, bb;
-        if (n_full > 0) load_iter<D, NS, VEC_SCALES, FL>(ba, K, V, sK, sV, roff(it), sub);
+        if (n_full > 0) load(ba, it);
         int k = 0;
         for (; k + 2 < n_full; k += 2) {
             const int it1 = nxt(it);
-            load_iter<D, NS, VEC_SCALES, FL>(bb, K, V, sK, sV, roff(it1), sub);
+            load(bb, it1);
             __builtin_amdgcn_sched_barrier(0);
-            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, 0, q, qscale, m, l, acc);
+            math(ba);
             it = nxt(it1);
-            load_iter<D, NS, VEC_SCALES, FL>(ba, K, V, sK, sV, roff(it), sub);
+            load(ba, it);
             __builtin_amdgcn_sched_barrier(0);
-            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, 0, q, qscale, m, l, acc);
+            math(bb);
         }
         if (n_full - k == 2) {
-            load_iter<D, NS, VEC_SCALES, FL>(bb, K, V, sK, sV, roff(nxt(it)), sub);
+            load(bb, nxt(it));
             __builtin_amdgcn_sched_barrier(0);
-            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, 0, q, qscale, m, l, acc);
-            decode_math<D, NS, false>(bb.kv, bb.vv, bb.sk, bb.sv, 0, 0, q, qscale, m, l, acc);
+            math(ba);
+            math(bb);
         } else if (n_full - k == 1) {
-            decode_math<D, NS, false>(ba.kv, ba.vv, ba.sk, ba.sv, 0, 0, q, qscale, m, l, acc);
+            math(ba);
         }
     } else {
         for (int k = 0; k < n_full; ++k) {
             IterBuf<NS> b;
-            load_iter<D, NS, VEC_SCALES, FL>(b, K, V, sK, sV, roff(it), sub);
-            decode_math<D, NS, false>(b.kv, b.vv, b.sk, b.sv, 0, 0, q, qscale, m, l, acc);
+            load(b, it);
+            math(b);
             it = nxt(it);
         }
     }
@@ -611,13 +664,16 @@ __global__ __launch_bounds__(64 * MAXW) void decode_block_kernel(
     const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
     const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
     const int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
-    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4)>(
-        Kbh, Vbh, sKbh, sVbh, [&](int i) { return (size_t)(j0 + i * G::kRowsPerIter + grp * NS); },
+    constexpr bool PAIRED = paired_rows(D, NS, MAXW);
+    constexpr int RS = PAIRED ? 2 : 1;
+    const int g0 = group_row0<PAIRED, NS>(grp);
+    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4), RS>(
+        Kbh, Vbh, sKbh, sVbh, [&](int i) { return (size_t)(j0 + i * G::kRowsPerIter + g0); },
         n_full, it, sub, q, qscale_l, m, l, acc);
     const int base = j0 + n_full * G::kRowsPerIter;
     if (base < j1)
-        decode_iter<D, NS, true, VEC_SCALES, FL>(Kbh, Vbh, sKbh, sVbh, base + grp * NS, j1, sub,
-                                                 q, qscale_l, m, l, acc);
+        decode_iter<D, NS, true, VEC_SCALES, FL, RS>(Kbh, Vbh, sKbh, sVbh, base + g0, j1, sub,
+                                                     q, qscale_l, m, l, acc);
     merge_block<D, MAXW>(m, l, acc, lane, grp, sub, w, nw, bh, s_ml, s_acc, out, qout, qscale);
 }
 
@@ -669,22 +725,27 @@ __global__ __launch_bounds__(64 * MAXW) void decode_paged_block_kernel(
     const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
     const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
     const int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
-    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4)>(
-        Kp, Vp, sKp, sVp, [&](int i) { return row_off(j0 + i * G::kRowsPerIter + grp * NS); },
+    // a group's rows (NS-aligned, or the 8-aligned pair block) share one page
+    constexpr bool PAIRED = paired_rows(D, NS, MAXW);
+    constexpr int RS = PAIRED ? 2 : 1;
+    const int g0 = group_row0<PAIRED, NS>(grp);
+    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4), RS>(
+        Kp, Vp, sKp, sVp, [&](int i) { return row_off(j0 + i * G::kRowsPerIter + g0); },
         n_full, it, sub, q, qscale_l, m, l, acc);
     const int base = j0 + n_full * G::kRowsPerIter;
     if (base < j1) {
-        const int row0 = base + grp * NS;
+        const int row0 = base + g0;
         IterBuf<NS> bt;
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
-            const size_t r = row_off(min(row0 + t, j1 - 1));
+            const size_t r = row_off(min(row0 + t * RS, j1 - 1));
             bt.kv[t] = load_kv16<(FL & kNtKV) != 0>(Kp + r * D + sub * 16);
             bt.vv[t] = load_kv16<(FL & kNtKV) != 0>(Vp + r * D + sub * 16);
             bt.sk[t] = load_f32<(FL & kNtScales) != 0>(sKp + r);
             bt.sv[t] = load_f32<(FL & kNtScales) != 0>(sVp + r);
         }
-        decode_math<D, NS, true>(bt.kv, bt.vv, bt.sk, bt.sv, row0, j1, q, qscale_l, m, l, acc);
+        decode_math<D, NS, true, RS>(bt.kv, bt.vv, bt.sk, bt.sv, row0, j1, q, qscale_l, m, l,
+                                     acc);
     }
     merge_block<D, MAXW>(m, l, acc, lane, grp, sub, w, nw, bh, s_ml, s_acc, out, qout, qscale);
 }
@@ -827,13 +888,17 @@ void launch_split(int flags, int stagger, dim3 grid, hipStream_t stream, const i
 #undef INT8K_SPLIT_LAUNCH
 }
 
+// The 8-wave instance takes the paired-row load flags where it pairs rows.
 template <int D, int NS, bool VEC>
-void launch_block(int flags, int stagger, int BH, hipStream_t stream, const int8_t* Q,
+void launch_block(const DecodeTuning& tn, int BH, hipStream_t stream, const int8_t* Q,
                   const int8_t* K, const int8_t* V, const float* sQ, const float* sK,
                   const float* sV, uint16_t* out, int8_t* qout, float* qs, int S, int S_cap,
                   const SplitPlan& plan, float qk) {
+    const int stagger = tn.stagger;
+    const bool eight = plan.nsplit <= 8;
+    const int flags = (eight && paired_rows(D, NS, 8)) ? tn.pair_flags : tn.flags;
 #define INT8K_BLOCK_LAUNCH(FLV)                                                               \
-    if (plan.nsplit <= 8)                                                                     \
+    if (eight)                                                                                \
         decode_block_kernel<D, NS, VEC, FLV, 8><<<(unsigned)BH, 64 * plan.nsplit, 0, stream>>>(  \
             Q, K, V, sQ, sK, sV, out, qout, qs, S, S_cap, plan.chunk, qk, stagger);           \
     else                                                                                      \
@@ -887,11 +952,11 @@ int launch_decode(const int8_t* Q, const int8_t* K, const int8_t* V, const Decod
     if (plan.nsplit <= kMaxBlockSplits && use_block_kernel()) {
         // one launch: the chunks of a (b,h) are the waves of one block
         if (ns == 4) {
-            if (vec) launch_block<D, 4, true>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
-            else launch_block<D, 4, false>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+            if (vec) launch_block<D, 4, true>(tn, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+            else launch_block<D, 4, false>(tn, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
         } else {
-            if (vec) launch_block<D, 8, true>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
-            else launch_block<D, 8, false>(fl, sg, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+            if (vec) launch_block<D, 8, true>(tn, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
+            else launch_block<D, 8, false>(tn, BH, stream, Q, K, V, sQ, sK, sV, out, o.q, o.qs, S, S_cap, plan, qk);
         }
         return check_launch("decode_block_kernel");
     }
@@ -943,7 +1008,8 @@ int launch_decode_paged(const int8_t* Q, const int8_t* Kp, const int8_t* Vp, con
             <<<(unsigned)BH, 64 * plan.nsplit, lds, stream>>>(                                 \
                 Q, Kp, Vp, sQ, sKp, sVp, tables, lens, out, o.q, o.qs, H, num_pages, log2_page, \
                 max_pages, (int)n_tab, plan.chunk, qk, st)
-        switch (tuning_for(D).flags & 3) {
+        const DecodeTuning tn = tuning_for(D);
+        switch ((paired_rows(D, NS, 8) ? tn.pair_flags : tn.flags) & 3) {
             case 0: INT8K_PAGED_BLOCK(0); break;
             case 1: INT8K_PAGED_BLOCK(1); break;
             case 2: INT8K_PAGED_BLOCK(2); break;
@@ -1098,6 +1164,14 @@ extern "C" size_t int8k_decode_attention_paged_workspace_bytes(int B, int H, int
     if (BH >= (1LL << 31)) return 0;
     const SplitPlan plan = plan_paged((int)BH, max_context, head_dim, nsplit);
     return carve(nullptr, BH * plan.nsplit, head_dim).bytes;
+}
+
+extern "C" int int8k_decode_attention_paged_num_splits(int B, int H, int max_context,
+                                                       int head_dim, int nsplit) {
+    if (B <= 0 || H <= 0 || max_context <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
+    const long long BH = (long long)B * H;
+    if (BH >= (1LL << 31)) return 0;
+    return plan_paged((int)BH, max_context, head_dim, nsplit).nsplit;
 }
 
 static int paged_impl(

@@ -52,6 +52,7 @@ _SIGNATURES = {
     "int8k_dequantize_per_token": (_I, [_P, _P, _I, _P, _P, _LL, _I, _P]),
     "int8k_kv_cache_append": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "int8k_decode_attention_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "int8k_decode_attention_paged_num_splits": (_I, [_I, _I, _I, _I, _I]),
     "int8k_layernorm_quantize_per_token": (_I, [_P, _I, _P, _P, _F, _P, _P, _P, _LL, _I, _P]),
     "int8k_quantize_heads": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "int8k_decode_attention_forward_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
@@ -402,6 +403,10 @@ def decode_attention_cache_quant(Qi, K_cache, V_cache, sQ, sK_cache, sV_cache, S
 
 def decode_paged_workspace_bytes(B, H, max_context, D, nsplit=0):
     return load().int8k_decode_attention_paged_workspace_bytes(B, H, max_context, D, nsplit)
+
+
+def decode_paged_num_splits(B, H, max_context, D, nsplit=0):
+    return load().int8k_decode_attention_paged_num_splits(B, H, max_context, D, nsplit)
 
 
 def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_tables,

@@ -66,6 +66,21 @@ def test_decode_split_plan(capi, BH, S, D):
         assert BH * ns >= 4096
 
 
+@pytest.mark.parametrize("B,H,S,D", [(1, 1, 1, 64), (8, 32, 32768, 64), (32, 32, 8192, 128),
+                                     (1, 2, 40000, 128)])
+def test_decode_paged_split_plan(capi, B, H, S, D):
+    ns = capi.decode_paged_num_splits(B, H, S, D)
+    assert 1 <= ns <= S
+    assert capi.decode_paged_workspace_bytes(B, H, S, D) >= B * H * ns * (D + 2) * 4
+    assert capi.decode_paged_num_splits(B, H, S, D, 1) == 1
+    assert capi.decode_paged_num_splits(B, H, S, D, 10 ** 6) <= S
+    assert capi.decode_paged_num_splits(0, H, S, D) == 0
+    assert capi.decode_paged_num_splits(B, H, S, 96) == 0
+    # the BASELINE shapes plan 8 chunks per (b,h): the one-launch paged kernel
+    if (B, H, S, D) in ((8, 32, 32768, 64), (32, 32, 8192, 128)):
+        assert ns == 8
+
+
 def test_prefill_argument_validation(capi):
     lib = capi.load()
     f = lambda **kw: lib.int8k_attention_forward(  # noqa: E731
