@@ -49,10 +49,13 @@ def test_paged_decode_via_torch_op(ext, gpu):
     assert_attn_close(out.float().cpu().numpy(), _oracle(c))
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("nsplit", [1, 2, 7, 64])
-def test_paged_decode_forced_splits(gpu, nsplit):
+def test_paged_decode_forced_splits(gpu, D, nsplit):
+    # up to 8 chunks: the one-launch kernel (paired rows at D=64, whose 8-row pair
+    # blocks must stay inside one page); 64: the split kernel and the combine
     lens = [1000, 64, 513]
-    c = workloads.paged_case(3, 2, 128, 32, lens, seed=nsplit, device=gpu)
+    c = workloads.paged_case(3, 2, D, 32, lens, seed=nsplit + D, device=gpu)
     out = capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
                                       c["sK_pages"], c["sV_pages"], c["block_tables"],
                                       c["context_lens"], c["max_context"], nsplit=nsplit)
