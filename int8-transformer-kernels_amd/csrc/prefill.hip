@@ -17,8 +17,7 @@
 // of the MFMA fragments and key scales are scheduled ahead of their uses.  The
 // wave index is read into a scalar register, so every per-wave condition of the
 // tile loop (causal skip, masked tile, fast or slow path) is a scalar branch.
-// Everything is
-// computed transposed so that each lane owns one query:
+// Everything is computed transposed so that each lane owns one query:
 //   S^T[64 keys x 32 q] = K . Q^T   on v_mfma_i32_32x32x32_i8 (A = K rows
 //                                   from LDS, B = Q kept in VGPRs)
 //   O^T[D x 32 q]      += V^T . P^T on v_mfma_f32_32x32x16_f16
