@@ -939,7 +939,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(decode shards over (b,h) with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(decode and prefill would shard over (b,h) with no exchange, the MLP over "
+              "d_ff with an all-reduce of the row maxima and of the output)", file=sys.stderr)
         sys.exit(2)
     if args.workload == "mlp":
         res = bench_mlp(args)
