@@ -70,6 +70,10 @@ inline int rows_per_iter(int D, int ns) { return (64 / (D / 16)) * ns; }
 // slot covers whole 128-byte lines; otherwise group g owns rows g*NS .. +NS-1.
 constexpr bool paired_rows(int D, int NS, int MAXW) { return D == 64 && NS == 4 && MAXW <= 8; }
 
+// Two register sets (the next iteration's loads in flight) in the 8-wave
+// one-launch kernels: at 4 slots, and at D = 128 with 8 slots.
+constexpr bool two_sets(int D, int NS, int MAXW) { return MAXW <= 8 && (NS == 4 || D == 128); }
+
 template <bool PAIRED, int NS>
 __device__ __forceinline__ int group_row0(int grp) {
     if constexpr (PAIRED) return 8 * (grp >> 1) + (grp & 1);
@@ -626,10 +630,12 @@ __device__ __forceinline__ void merge_block(float m, float l, float* acc, int la
 // LDS; wave 0 then merges the chunks with the log-sum-exp rule and writes the
 // row.  No partial state leaves the chip and there is no second launch.
 // MAXW: the most waves the instance is launched with (8 or kMaxBlockSplits).
-// The 8-wave instance has twice the registers per wave, which lets NSLOT = 4
-// keep the next iteration's loads in flight (a second register set) while the
-// current one computes: a short chunk is only a few dependent load rounds, so
-// their latency would show.
+// The 8-wave instance has twice the registers per wave, which lets it keep the
+// next iteration's loads in flight (a second register set, two_sets) while the
+// current one computes: at 4 slots a short chunk is only a few dependent load
+// rounds, so their latency would show; at D = 128 with 8 slots (204 VGPRs, two
+// waves per SIMD) the stream then runs at fewer waves per CU with the same
+// bytes in flight, which the HBM read rate prefers.
 template <int D, int NS, bool VEC_SCALES, int FL, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void decode_block_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K,
@@ -667,7 +673,7 @@ __global__ __launch_bounds__(64 * MAXW) void decode_block_kernel(
     constexpr bool PAIRED = paired_rows(D, NS, MAXW);
     constexpr int RS = PAIRED ? 2 : 1;
     const int g0 = group_row0<PAIRED, NS>(grp);
-    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4), RS>(
+    walk_iters<D, NS, VEC_SCALES, FL, two_sets(D, NS, MAXW), RS>(
         Kbh, Vbh, sKbh, sVbh, [&](int i) { return (size_t)(j0 + i * G::kRowsPerIter + g0); },
         n_full, it, sub, q, qscale_l, m, l, acc);
     const int base = j0 + n_full * G::kRowsPerIter;
@@ -729,7 +735,7 @@ __global__ __launch_bounds__(64 * MAXW) void decode_paged_block_kernel(
     constexpr bool PAIRED = paired_rows(D, NS, MAXW);
     constexpr int RS = PAIRED ? 2 : 1;
     const int g0 = group_row0<PAIRED, NS>(grp);
-    walk_iters<D, NS, VEC_SCALES, FL, (MAXW <= 8 && NS == 4), RS>(
+    walk_iters<D, NS, VEC_SCALES, FL, two_sets(D, NS, MAXW), RS>(
         Kp, Vp, sKp, sVp, [&](int i) { return row_off(j0 + i * G::kRowsPerIter + g0); },
         n_full, it, sub, q, qscale_l, m, l, acc);
     const int base = j0 + n_full * G::kRowsPerIter;
