@@ -233,6 +233,8 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
     512 MB cycle through enough copies of the cache (at least 3, 768 MB in total) that the
     256 MB Infinity Cache cannot serve a step from the previous one.  Every (b,h) row of
     the output is checked against the C oracle."""
+    import ctypes
+
     import numpy as np
     import torch
 
@@ -255,12 +257,22 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
     out = torch.empty((BH, D), dtype=torch.float16, device=dev)
     ws = torch.empty(max(capi.decode_workspace_bytes(BH, S, D, args.nsplit), 1),
                      dtype=torch.uint8, device=dev)
+    # A step is one call of the C ABI entry point with its arguments built once per
+    # cache copy, as a serving loop holds them: the Python wrapper's per-call checks
+    # would otherwise set the time of the short steps (config 1's kernel takes ~6 us).
+    fn = capi.load().int8k_decode_attention_forward
+    Pt = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(stream.cuda_stream)
+    calls = [(Pt(Q), Pt(K), Pt(V), Pt(out), Pt(sQ), Pt(sK), Pt(sV), BH, S, D, args.nsplit,
+              Pt(ws), ws.numel(), st) for (K, V, sK, sV) in copies]
     it = [0]
 
     def step():
-        K, V, sK, sV = copies[it[0] % n_copies]
+        a = calls[it[0] % n_copies]
         it[0] += 1
-        capi.decode_attention(Q, K, V, sQ, sK, sV, nsplit=args.nsplit, out=out, workspace=ws)
+        rc = fn(*a)
+        if rc != 0:
+            capi.check("int8k_decode_attention_forward", rc)
 
     ms, windows = time_windows(step, args.steps, args.warmup, stream)
     K, V, sK, sV = kv

@@ -97,6 +97,11 @@ struct SplitPlan {
 // Most chunks per (b,h) that run as one launch (decode_block_kernel: one wave
 // per chunk, merged in LDS); larger plans run the split + combine pair.
 constexpr int kMaxBlockSplits = 16;
+// The automatic plan never picks 9..16 chunks: those would run the 16-wave
+// instance (one register set), and 8 chunks on the 8-wave instance (two
+// register sets, paired rows at D=64) measured 2-27% faster at every shape
+// tried (B1 H12 D64 1K to B16 H32 D128 8K).  Forced split counts still may.
+constexpr int kMaxAutoBlockSplits = 8;
 // Largest page-id table the paged one-launch kernel stages in LDS (12288 ids);
 // longer tables run the paged split + combine pair.
 constexpr long long kPagedLdsTableBytes = 48 << 10;
@@ -155,11 +160,12 @@ SplitPlan plan_splits(int BH, int S, int D, int nsplit_req) {
     } else {
         ns = ceil_div(tn.target_units, BH);
         // keep at least 4 iterations per unit unless S is short; an under-filled
-        // grid (few (b,h)) may still take up to kMaxBlockSplits one-iteration
-        // chunks, which the one-launch kernel merges on chip
+        // grid (few (b,h)) may still take up to kMaxAutoBlockSplits short chunks,
+        // which the one-launch kernel merges on chip
         const long long by_len = std::max<long long>(
-            1, std::max(ceil_div(S, 4LL * R), std::min<long long>(kMaxBlockSplits, ceil_div(S, R))));
+            1, std::max(ceil_div(S, 4LL * R), std::min<long long>(kMaxAutoBlockSplits, ceil_div(S, R))));
         ns = std::min(ns, by_len);
+        if (ns > kMaxAutoBlockSplits && ns <= kMaxBlockSplits) ns = kMaxAutoBlockSplits;
     }
     ns = std::max<long long>(1, std::min(ns, max_split));
     long long chunk = round_up((size_t)ceil_div(S, ns), (size_t)R);
