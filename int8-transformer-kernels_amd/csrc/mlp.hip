@@ -767,19 +767,68 @@ __global__ __launch_bounds__(256) void tensor_absmax_kernel(const float* __restr
     if (threadIdx.x == 0) *out = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// dst[C][R] = src[R][C]^T through a 64x64 LDS tile.
+// dst[C][R] = src[R][C]^T in 128 x 128-byte tiles.  Interior tiles of 16-byte
+// aligned matrices (vec): each thread loads 16 bytes of 4 source rows (8 threads
+// cover a row's 128 bytes), the tile goes to LDS as dwords (row stride 33
+// dwords), each thread reads the 4-column dwords of 16 source rows, transposes
+// them in 4 x 4 byte blocks with v_perm, and stores 16 bytes of 4 destination
+// rows (8 threads cover a row's 128 bytes).  Other tiles go byte by byte.
+constexpr int kTrTile = 128;
+constexpr int kTrStride = kTrTile / 4 + 1;  // LDS dwords per source row
+
 __global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ src,
-                                                           int8_t* __restrict__ dst, int R, int C) {
-    __shared__ int8_t tile[64][65];
-    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const int r = i / 64, c = i % 64;
-        if (r0 + r < R && c0 + c < C) tile[r][c] = src[(size_t)(r0 + r) * C + c0 + c];
+                                                           int8_t* __restrict__ dst, int R, int C,
+                                                           int vec_ok) {
+    __shared__ uint32_t tile[kTrTile * kTrStride];
+    const int r0 = blockIdx.y * kTrTile, c0 = blockIdx.x * kTrTile;
+    const int t = threadIdx.x;
+    if (vec_ok && r0 + kTrTile <= R && c0 + kTrTile <= C) {
+        const int cw = (t & 7) * 4;  // first dword of this thread's 16 bytes
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = (t >> 3) + 32 * i;
+            const uint4 v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + r) * C + c0 + 4 * cw);
+            uint32_t* row = tile + r * kTrStride + cw;
+            row[0] = v.x;
+            row[1] = v.y;
+            row[2] = v.z;
+            row[3] = v.w;
+        }
+        __syncthreads();
+        // destination rows 4a .. 4a+3 (source columns), bytes = source rows 16b .. 16b+15
+        const int a = t >> 3, b = t & 7;
+        uint32_t w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = tile[(16 * b + i) * kTrStride + a];
+        uint32_t o[4][4];  // [destination row j][dword g: source rows 16b + 4g .. +3]
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            // {w0.bk, w1.bk, w0.bk', w1.bk'} pairs, then the 4-byte column of byte j
+            const uint32_t lo01 = __builtin_amdgcn_perm(w[4 * g + 1], w[4 * g], 0x05010400u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(w[4 * g + 1], w[4 * g], 0x07030602u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(w[4 * g + 3], w[4 * g + 2], 0x05010400u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(w[4 * g + 3], w[4 * g + 2], 0x07030602u);
+            o[0][g] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+            o[1][g] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+            o[2][g] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+            o[3][g] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint4*>(dst + (size_t)(c0 + 4 * a + j) * R + r0 + 16 * b) =
+                make_uint4(o[j][0], o[j][1], o[j][2], o[j][3]);
+        return;
+    }
+    int8_t* tb = reinterpret_cast<int8_t*>(tile);
+    constexpr int kB = kTrStride * 4;  // bytes per LDS row
+    for (int i = t; i < kTrTile * kTrTile; i += 256) {
+        const int r = i / kTrTile, c = i % kTrTile;
+        if (r0 + r < R && c0 + c < C) tb[r * kB + c] = src[(size_t)(r0 + r) * C + c0 + c];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const int c = i / 64, r = i % 64;
-        if (r0 + r < R && c0 + c < C) dst[(size_t)(c0 + c) * R + r0 + r] = tile[r][c];
+    for (int i = t; i < kTrTile * kTrTile; i += 256) {
+        const int c = i / kTrTile, r = i % kTrTile;
+        if (r0 + r < R && c0 + c < C) dst[(size_t)(c0 + c) * R + r0 + r] = tb[r * kB + c];
     }
 }
 
@@ -794,8 +843,9 @@ int launch_gemm(const int8_t* A, const int8_t* Bt, int M, int N, int K, const Ep
 }
 
 int launch_transpose(const int8_t* src, int8_t* dst, int R, int C, hipStream_t stream) {
-    const dim3 grid((C + 63) / 64, (R + 63) / 64);
-    transpose_i8_kernel<<<grid, 256, 0, stream>>>(src, dst, R, C);
+    const dim3 grid((C + kTrTile - 1) / kTrTile, (R + kTrTile - 1) / kTrTile);
+    const int vec_ok = R % 16 == 0 && C % 16 == 0 && aligned_to(src, 16) && aligned_to(dst, 16);
+    transpose_i8_kernel<<<grid, 256, 0, stream>>>(src, dst, R, C, vec_ok);
     return check_launch("transpose_i8_kernel");
 }
 

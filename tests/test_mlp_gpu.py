@@ -169,6 +169,19 @@ def test_mlp_prepacked_matches_unpacked(ext, gpu):
     assert torch.equal(a, b) and sa == sb
 
 
+@pytest.mark.parametrize("dm,dff", [(512, 2048), (200, 300), (64, 129), (1000, 1040), (130, 4096),
+                                    (33, 17)])
+def test_transpose_int8_weights_shapes(gpu, dm, dff):
+    # 128 x 128 tiles: interior tiles of 16-byte aligned matrices take the vector path,
+    # edge tiles and other shapes the byte path; both give the exact transposes
+    g = torch.Generator(device=gpu).manual_seed(dm * 7 + dff)
+    W1 = torch.randint(-128, 128, (dm, dff), dtype=torch.int8, device=gpu, generator=g)
+    W2 = torch.randint(-128, 128, (dff, dm), dtype=torch.int8, device=gpu, generator=g)
+    W1T, W2T = capi.transpose_int8_weights(W1, W2)
+    torch.cuda.synchronize()
+    assert torch.equal(W1T, W1.t().contiguous()) and torch.equal(W2T, W2.t().contiguous())
+
+
 def test_mlp_kats_zero_and_constant(ext, gpu):
     T, dm, dff = 256, 256, 512
     z = torch.zeros(1, T, dm, dtype=torch.int8, device=gpu)
