@@ -66,6 +66,18 @@ def test_decode_split_plan(capi, BH, S, D):
         assert BH * ns >= 4096
 
 
+def test_decode_auto_plans_skip_9_to_16_chunks(capi):
+    # automatic plans take at most 8 chunks per (b,h) on the one-launch kernel (the 8-wave
+    # instance) or more than 16 on the split kernel; forced counts of 9..16 are honoured
+    for D in (64, 128):
+        for BH in (1, 2, 12, 32, 64, 128, 256, 384, 512, 1024, 4096):
+            for S in (1, 63, 64, 100, 1024, 2048, 3000, 4096, 8192, 16384, 40000, 131072):
+                ns = capi.decode_num_splits(BH, S, D)
+                assert 1 <= ns <= 8 or ns > 16, (BH, S, D, ns)
+        assert capi.decode_num_splits(12, 1024, D, 16) == 16
+    assert capi.decode_num_splits(12, 1024, 64) == 8
+
+
 @pytest.mark.parametrize("B,H,S,D", [(1, 1, 1, 64), (8, 32, 32768, 64), (32, 32, 8192, 128),
                                      (1, 2, 40000, 128)])
 def test_decode_paged_split_plan(capi, B, H, S, D):
