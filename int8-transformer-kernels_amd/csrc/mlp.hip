@@ -674,8 +674,12 @@ __global__ __launch_bounds__(256) void requant_rows_kernel(
         return static_cast<int>(__builtin_rintf(fminf(fmaxf(f, -128.f), 127.f)));
     };
     if ((N & 7) == 0 && (ldh & 7) == 0 && (ldq & 7) == 0) {
+        // the fp16 rows are read once, here (non-temporal), and several loads per
+        // thread go out before the first one is used
+        typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+#pragma unroll 4
         for (int c = threadIdx.x * 8; c < N; c += 256 * 8) {
-            const uint4 v = *reinterpret_cast<const uint4*>(hr + c);
+            const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(hr + c));
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
             uint32_t lo = 0, hi = 0;
 #pragma unroll
