@@ -29,7 +29,9 @@
 // splitk_epilogue_kernel<EPI> (sums the partials per row, then the same
 // epilogue math as gemm_i8_kernel, writing the same fp16 output and absmax
 // partials), so requant_rows_kernel and every result are the same on both
-// paths.
+// paths.  Above 512 rows, a GEMM whose 256 x 256 grid has at most 128 tiles runs
+// gemm_i8_mid_kernel<EPI> (128 x 128 tiles, two blocks per CU, the same
+// epilogue), e.g. GEMM2 at T = 4096, d_model 1024.
 #include <algorithm>
 #include <cstdlib>
 
@@ -110,15 +112,15 @@ __device__ __forceinline__ void tile_rowmax(const float (&rmax)[16], int* slot, 
     }
 }
 
-// Interior tiles (every row and column in range, BM * ldc * 2 < 2^32): the
+// Interior tiles (every row and column in range, tile rows * ldc * 2 < 2^32): the
 // fp16 tile goes out through a buffer resource at the tile's corner, so each
 // store's address is the lane's fixed offset plus a uniform (scalar) one.
 // Rows r, r+1 of a column sit in one lane and columns c, c+1 in lanes 2k,
 // 2k+1: the lane converts its pair of rows into one word (v_cvt_pk_f16_f32),
 // swaps it with the neighbour lane (DPP), and one byte permute leaves the
 // even lane (r, c..c+1) and the odd lane (r+1, c..c+1) to store as one dword.
-template <int EPI>
-__device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM][TN], const EpiParams& p,
+template <int EPI, int TM_ = TM, int TN_ = TN, int WM_ = WM, int WN_ = WN, int BM_ = BM>
+__device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM_][TN_], const EpiParams& p,
                                                   int m0, int n0, int* rowmax, const float* esa,
                                                   const float* esb, const float* ebias) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -128,31 +130,31 @@ __device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM][TN], con
     const int wm = wave >> 1, wn = wave & 1;
     const bool odd = lane & 1;
     const __amdgpu_buffer_rsrc_t out =
-        make_buffer(p.c16 + (size_t)m0 * p.ldc + n0, (uint32_t)(BM * p.ldc * 2));
+        make_buffer(p.c16 + (size_t)m0 * p.ldc + n0, (uint32_t)(BM_ * p.ldc * 2));
     const uint32_t voff =
-        ((uint32_t)(wm * WM + (lane >> 5) * 4 + (odd ? 1 : 0)) * p.ldc + wn * WN + (lane & 30)) * 2;
+        ((uint32_t)(wm * WM_ + (lane >> 5) * 4 + (odd ? 1 : 0)) * p.ldc + wn * WN_ + (lane & 30)) * 2;
     const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
-    float sbv[TN], biv[TN];
+    float sbv[TN_], biv[TN_];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        sbv[j] = esb[wn * WN + j * 32 + (lane & 31)];
-        biv[j] = ebias[wn * WN + j * 32 + (lane & 31)];
+    for (int j = 0; j < TN_; ++j) {
+        sbv[j] = esb[wn * WN_ + j * 32 + (lane & 31)];
+        biv[j] = ebias[wn * WN_ + j * 32 + (lane & 31)];
     }
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM_; ++i) {
         // rows (r/4)*8 + (lane/32)*4 + r%4: four runs of 4 consecutive rows
         float sav[16], rmax[16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float4 s4 =
-                *reinterpret_cast<const float4*>(esa + wm * WM + i * 32 + q * 8 + (lane >> 5) * 4);
+                *reinterpret_cast<const float4*>(esa + wm * WM_ + i * 32 + q * 8 + (lane >> 5) * 4);
             sav[4 * q] = s4.x, sav[4 * q + 1] = s4.y, sav[4 * q + 2] = s4.z, sav[4 * q + 3] = s4.w;
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
-        uint32_t words[TN][8];  // packed fp16 pairs, stored once all TN are done
+        uint32_t words[TN_][8];  // packed fp16 pairs, stored once all column tiles are done
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
+        for (int j = 0; j < TN_; ++j) {
             // stage by stage over the 16 elements, so one wave per SIMD has
             // independent work between the dependent steps of each element
             float v[16];
@@ -181,50 +183,50 @@ __device__ __forceinline__ void epilogue_interior(const v16i (&acc)[TM][TN], con
                 words[j][r >> 1] = __builtin_amdgcn_perm(nb, own, sel);
             }
         }
-        // row by row, the TN stores of a row back to back: the 64-byte pieces
+        // row by row, the column tiles' stores of a row back to back: the 64-byte pieces
         // of each 128-byte line reach the cache together
 #pragma unroll
         for (int r = 0; r < 16; r += 2)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
+            for (int j = 0; j < TN_; ++j) {
                 const uint32_t soff = ((uint32_t)(i * 32 + (r >> 2) * 8 + (r & 3)) * p.ldc + j * 32) * 2;
                 __builtin_amdgcn_raw_buffer_store_b32(words[j][r >> 1], out, voff, soff, 0);
             }
-        tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
+        tile_rowmax(rmax, rowmax + wn * BM_ + wm * WM_ + i * 32, lane);
     }
 }
 
 // Tiles on the matrix edge: the same values, element stores guarded by row < M
 // and column < N, and the row maxima over in-range columns only.
-template <int EPI>
-__device__ __forceinline__ void epilogue_edge(const v16i (&acc)[TM][TN], const EpiParams& p,
+template <int EPI, int TM_ = TM, int TN_ = TN, int WM_ = WM, int WN_ = WN, int BM_ = BM>
+__device__ __forceinline__ void epilogue_edge(const v16i (&acc)[TM_][TN_], const EpiParams& p,
                                               int M, int N, int m0, int n0, int* rowmax,
                                               const float* esa, const float* esb,
                                               const float* ebias) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int rbase = m0 + wm * WM;
-    const int cbase = n0 + wn * WN + (lane & 31);
+    const int rbase = m0 + wm * WM_;
+    const int cbase = n0 + wn * WN_ + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM_; ++i) {
         float rmax[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int cl = wn * WN + j * 32 + (lane & 31);
+        for (int j = 0; j < TN_; ++j) {
+            const int cl = wn * WN_ + j * 32 + (lane & 31);
             const bool cok = n0 + cl < N;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int rl = wm * WM + i * 32 + acc_row(r, lane);
+                const int rl = wm * WM_ + i * 32 + acc_row(r, lane);
                 const float v = epi_value<EPI>(acc[i][j][r], esa[rl], esb[cl], ebias[cl]);
                 if (cok) rmax[r] = fmaxf(rmax[r], fabsf(v));
                 const int row = rbase + i * 32 + acc_row(r, lane);
                 if (row < M && cok) p.c16[(size_t)row * p.ldc + cbase + j * 32] = f32_to_f16_bits(v);
             }
         }
-        tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
+        tile_rowmax(rmax, rowmax + wn * BM_ + wm * WM_ + i * 32, lane);
     }
 }
 
@@ -232,32 +234,39 @@ __device__ __forceinline__ void epilogue_edge(const v16i (&acc)[TM][TN], const E
 // absmax partial pmax[tn][row].  pre_sa/pre_sb/pre_b: this thread's row scale
 // (row m0 + t), column scale and bias (column n0 + t), loaded before the main
 // loop so it hides their latency.
-template <int EPI>
-__device__ __forceinline__ void epilogue_tile(const v16i (&acc)[TM][TN], const EpiParams& p, int M,
-                                              int N, int m0, int n0, int tn, float pre_sa,
+template <int EPI, int TM_ = TM, int TN_ = TN, int WM_ = WM, int WN_ = WN, int BM_ = BM,
+          int kScaleOff = LDS_BYTES>
+__device__ __forceinline__ void epilogue_tile(const v16i (&acc)[TM_][TN_], const EpiParams& p,
+                                              int M, int N, int m0, int n0, int tn, float pre_sa,
                                               float pre_sb, float pre_b, char* lds) {
     // Row absmax of this block's tile: rowmax[wn][row] from each column
     // half of the waves, combined below (values >= 0, so integer max on
     // the bit pattern orders them like floats).  The scale region lies
     // past the stages; the row maxima reuse stage 0, whose last reads
-    // (operands past the end of K) are never used.
+    // (operands past the end of K) are never used.  Square tiles of BM_
+    // rows; threads t < BM_ hold row t's scale and column t's scale and bias.
+    static_assert(BM_ <= kThreads && 2 * WM_ == BM_ && 2 * WN_ == BM_, "2 x 2 waves");
     int* rowmax = reinterpret_cast<int*>(lds);
-    float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
-    float* esb = esa + BM;
-    float* ebias = esb + BN;
-    esa[threadIdx.x] = pre_sa;
-    esb[threadIdx.x] = pre_sb;
-    ebias[threadIdx.x] = pre_b;
+    float* esa = reinterpret_cast<float*>(lds + kScaleOff);
+    float* esb = esa + BM_;
+    float* ebias = esb + BM_;
+    const bool holder = BM_ == kThreads || (int)threadIdx.x < BM_;
+    if (holder) {
+        esa[threadIdx.x] = pre_sa;
+        esb[threadIdx.x] = pre_sb;
+        ebias[threadIdx.x] = pre_b;
+    }
     __syncthreads();
-    if (m0 + BM <= M && n0 + BN <= N && (size_t)BM * p.ldc * 2 < (1ull << 32))
-        epilogue_interior<EPI>(acc, p, m0, n0, rowmax, esa, esb, ebias);
+    if (m0 + BM_ <= M && n0 + BM_ <= N && (size_t)BM_ * p.ldc * 2 < (1ull << 32))
+        epilogue_interior<EPI, TM_, TN_, WM_, WN_, BM_>(acc, p, m0, n0, rowmax, esa, esb, ebias);
     else
-        epilogue_edge<EPI>(acc, p, M, N, m0, n0, rowmax, esa, esb, ebias);
+        epilogue_edge<EPI, TM_, TN_, WM_, WN_, BM_>(acc, p, M, N, m0, n0, rowmax, esa, esb,
+                                                     ebias);
     __syncthreads();
     const int row = m0 + threadIdx.x;
-    if (row < M)
+    if (holder && row < M)
         p.pmax[(size_t)tn * M + row] =
-            __int_as_float(max(rowmax[threadIdx.x], rowmax[BM + threadIdx.x]));
+            __int_as_float(max(rowmax[threadIdx.x], rowmax[BM_ + threadIdx.x]));
 }
 
 template <int EPI>
@@ -305,6 +314,123 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     } else {
         epilogue_tile<EPI>(acc, p, M, N, m0, n0, tn, pre_sa, pre_sb, pre_b, lds);
     }
+}
+
+// ------------------------------------------------------------ mid-size grids
+// gemm_i8_mid_kernel<EPI>: 128 x 128 output tiles for GEMMs whose 256 x 256
+// grid leaves CUs idle (T = 4096 at d_model 1024: GEMM2 has 16 x 4 big tiles
+// for 256 CUs).  Four waves in a 2 x 2 grid each own 64 x 64 (2 x 2 MFMA
+// tiles of 32 x 32 x 32); A and Bt go global -> VGPR -> LDS in the big
+// kernel's padded layout, double-buffered, the next K-step's loads in flight
+// during the current one.  75 KiB of LDS: two blocks per CU, whose waves hide
+// each other's waits.  Half the MFMA work per fragment read of the big tile,
+// so it runs only where the big grid is too small.  Same epilogue code and
+// bytes as gemm_i8_kernel, with one absmax partial per row and 128 columns.
+constexpr int kMidB = 128, kMidW = 64, kMidT = kMidW / 32;
+constexpr int kMidAStage = kMidB * LDS_STRIDE;
+constexpr int kMidStage = 2 * kMidAStage;
+constexpr int kMidLds = 2 * kMidStage;
+constexpr int kMidEpiLds = kMidLds + 3 * kMidB * 4;
+constexpr int kMidChunks = kMidB * kChunksPerRow / kThreads;
+static_assert(kMidChunks == 4 && 2 * kMidEpiLds <= 160 * 1024, "two blocks per CU");
+
+template <bool EDGE>
+__device__ __forceinline__ void mid_mainloop(v16i (&acc)[kMidT][kMidT],
+                                             const int8_t* __restrict__ A,
+                                             const int8_t* __restrict__ Bt, int M, int N, int K,
+                                             int m0, int n0, char* lds) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+    for (int i = 0; i < kMidT; ++i)
+#pragma unroll
+        for (int j = 0; j < kMidT; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    const int nk = (K + BK - 1) / BK;
+    const int a_off = (wm * kMidW + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    const int b_off = kMidAStage + (wn * kMidW + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    int4 fa[kMidChunks], fb[kMidChunks];
+    // chunk c = t + 256 i of a 128 x 128-byte operand tile: row c / 8, bytes (c % 8) * 16;
+    // rows past the matrix and K past the end load clamped addresses, zeroed on EDGE
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < kMidChunks; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+            const int gk = min(k0 + kc, K - 16);
+            fa[i] = *reinterpret_cast<const int4*>(A + (size_t)min(m0 + row, M - 1) * K + gk);
+            fb[i] = *reinterpret_cast<const int4*>(Bt + (size_t)min(n0 + row, N - 1) * K + gk);
+        }
+    };
+    auto store = [&](char* stage, int k0) {
+#pragma unroll
+        for (int i = 0; i < kMidChunks; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            const int row = c / kChunksPerRow, kc = (c % kChunksPerRow) * 16;
+            int4 va = fa[i], vb = fb[i];
+            if constexpr (EDGE) {
+                const bool kok = k0 + kc < K;
+                if (!(kok && m0 + row < M)) va = make_int4(0, 0, 0, 0);
+                if (!(kok && n0 + row < N)) vb = make_int4(0, 0, 0, 0);
+            }
+            *reinterpret_cast<int4*>(stage + row * LDS_STRIDE + kc) = va;
+            *reinterpret_cast<int4*>(stage + kMidAStage + row * LDS_STRIDE + kc) = vb;
+        }
+    };
+    load(0);
+    store(lds, 0);
+    if (nk > 1) load(BK);
+    __syncthreads();
+    // Step kt reads buffer kt & 1 and writes buffer (kt + 1) & 1, whose last
+    // reads (step kt - 1) finished before that step's barrier.
+    for (int kt = 0; kt < nk; ++kt) {
+        const char* cur = lds + (kt & 1) * kMidStage;
+#pragma unroll
+        for (int s = 0; s < BK / 32; ++s) {
+            v4i a[kMidT], b[kMidT];
+#pragma unroll
+            for (int i = 0; i < kMidT; ++i)
+                a[i] = *reinterpret_cast<const v4i*>(cur + a_off + i * 32 * LDS_STRIDE + s * 32);
+#pragma unroll
+            for (int j = 0; j < kMidT; ++j)
+                b[j] = *reinterpret_cast<const v4i*>(cur + b_off + j * 32 * LDS_STRIDE + s * 32);
+#pragma unroll
+            for (int i = 0; i < kMidT; ++i)
+#pragma unroll
+                for (int j = 0; j < kMidT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0,
+                                                                      0);
+        }
+        if (kt + 1 < nk) store(lds + ((kt + 1) & 1) * kMidStage, (kt + 1) * BK);
+        if (kt + 2 < nk) load((kt + 2) * BK);
+        __syncthreads();
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 2) void gemm_i8_mid_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int M, int N, int K,
+    int tiles_m, int tiles_n, EpiParams p) {
+    static_assert(EPI != EPI_I32, "fused epilogues only");
+    extern __shared__ __align__(16) char lds[];
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * kMidB, n0 = tn * kMidB;
+    // threads t and t + 128 load row / column t's scales (clamped, unconditional);
+    // the epilogue keeps those of t < 128
+    const int t = threadIdx.x & (kMidB - 1);
+    const float pre_sa = p.sa[(size_t)min(m0 + t, M - 1) * p.sa_stride];
+    const float pre_sb = p.sb[(size_t)min(n0 + t, N - 1) * p.sb_stride];
+    const float pre_b = p.bias != nullptr ? p.bias[min(n0 + t, N - 1)] : 0.f;
+    v16i acc[kMidT][kMidT];
+    if (m0 + kMidB <= M && n0 + kMidB <= N && K % BK == 0)
+        mid_mainloop<false>(acc, A, Bt, M, N, K, m0, n0, lds);
+    else
+        mid_mainloop<true>(acc, A, Bt, M, N, K, m0, n0, lds);
+    epilogue_tile<EPI, kMidT, kMidT, kMidW, kMidW, kMidB, kMidLds>(acc, p, M, N, m0, n0, tn,
+                                                                   pre_sa, pre_sb, pre_b, lds);
 }
 
 // The MLP's GEMM2 over the fp16 hidden A16 [M][K] itself, with no
@@ -495,10 +621,6 @@ inline bool use_skinny(int M, int N, int K) {
     return mnk <= (1LL << 31) || (M > 4 * kSkM && big_tiles < 64 && mnk <= (1LL << 32));
 }
 
-// Absmax partials per row that the GEMM's epilogue leaves (requant reads them).
-inline int epi_tiles(int M, int N, int K) {
-    return use_skinny(M, N, K) ? N / kSkinnyN : (N + BN - 1) / BN;
-}
 
 __device__ __forceinline__ void skinny_load(v4i (&b)[4], v4i (&a)[4], const int8_t* arow,
                                             const int8_t* brow, int k) {
@@ -620,6 +742,25 @@ inline SplitKPlan splitk_plan(int M, int N, int K) {
     pl.splits = (K + pl.k_per_split - 1) / pl.k_per_split;
     pl.use = true;
     return pl;
+}
+
+// The 128 x 128 kernel takes the GEMMs that the few-token paths leave and whose
+// 256 x 256 grid has at most 128 tiles: then its 4x as many tiles fit one round
+// of two blocks on each of the 256 CUs.  Measured per MLP (d_model 1024, d_ff
+// 4096, prepacked): T = 2048 86 -> 57 us, T = 4096 99 -> 82 us, T = 8192 (128
+// big tiles in GEMM2) 145 -> 140 us; at 192 big tiles (T = 12288) it lost 11%.
+constexpr int kMidMaxBigTiles = 128;
+
+inline bool use_mid(int M, int N, int K) {
+    if (use_skinny(M, N, K) || splitk_plan(M, N, K).use) return false;
+    const long long big_tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    return big_tiles <= kMidMaxBigTiles;
+}
+
+// Absmax partials per row that the GEMM's epilogue leaves (requant reads them).
+inline int epi_tiles(int M, int N, int K) {
+    if (use_skinny(M, N, K)) return N / kSkinnyN;
+    return use_mid(M, N, K) ? (N + kMidB - 1) / kMidB : (N + BN - 1) / BN;
 }
 
 inline size_t splitk_partial_bytes(int M, int N, int K) {
@@ -846,6 +987,15 @@ int launch_gemm(const int8_t* A, const int8_t* Bt, int M, int N, int K, const Ep
     return check_launch("gemm_i8_kernel");
 }
 
+template <int EPI>
+int launch_gemm_mid(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
+                    hipStream_t stream) {
+    const int tiles_m = (M + kMidB - 1) / kMidB, tiles_n = (N + kMidB - 1) / kMidB;
+    gemm_i8_mid_kernel<EPI><<<tiles_m * tiles_n, kThreads, kMidEpiLds, stream>>>(
+        A, Bt, M, N, K, tiles_m, tiles_n, p);
+    return check_launch("gemm_i8_mid_kernel");
+}
+
 int launch_transpose(const int8_t* src, int8_t* dst, int R, int C, hipStream_t stream) {
     const dim3 grid((C + kTrTile - 1) / kTrTile, (R + kTrTile - 1) / kTrTile);
     const int vec_ok = R % 16 == 0 && C % 16 == 0 && aligned_to(src, 16) && aligned_to(dst, 16);
@@ -920,6 +1070,12 @@ int configure_lds() {
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)gemm_i8_a16_kernel,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kA16LdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_mid_kernel<EPI_GELU_F16>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kMidEpiLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_mid_kernel<EPI_F16>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kMidEpiLds);
         if (e != hipSuccess) {
             set_last_error("hipFuncSetAttribute", e);
             return (int)INT8K_ERR_HIP;
@@ -1013,6 +1169,8 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
         st = launch_gemm_skinny<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     else if (sk1.use)
         st = launch_gemm_splitk<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, sk1, w.part, p1, s);
+    else if (use_mid(T, d_ff, d_model))
+        st = launch_gemm_mid<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     else
         st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     if (st != INT8K_OK) return st;
@@ -1028,7 +1186,9 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p2.pmax = w.p2;
     const SplitKPlan sk2 = splitk_plan(T, d_model, d_ff);
     const bool skinny2 = use_skinny(T, d_model, d_ff);
-    if (!skinny2 && !sk2.use && gemm2_reads_fp16_hidden()) {
+    // the on-load path has 256 x 256 tiles on every grid it runs
+    const bool a16 = !skinny2 && !sk2.use && gemm2_reads_fp16_hidden();
+    if (a16) {
         // the tiled GEMM2 reads the fp16 hidden and quantizes it per row on load
         const int tiles_m = (T + BM - 1) / BM, tiles_n = (d_model + BN - 1) / BN;
         gemm_i8_a16_kernel<<<tiles_m * tiles_n, kThreads, kA16LdsBytes, s>>>(
@@ -1044,11 +1204,13 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
             st = launch_gemm_skinny<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
         else if (sk2.use)
             st = launch_gemm_splitk<EPI_F16>(w.hq, W2t, T, d_model, d_ff, sk2, w.part, p2, s);
+        else if (use_mid(T, d_model, d_ff))
+            st = launch_gemm_mid<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
         else
             st = launch_gemm<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
         if (st != INT8K_OK) return st;
     }
-    const int tn2 = epi_tiles(T, d_model, d_ff);
+    const int tn2 = a16 ? (d_model + BN - 1) / BN : epi_tiles(T, d_model, d_ff);
     const float* tmax = nullptr;
     if (per_tensor_out) {
         tensor_absmax_kernel<<<1, 256, 0, s>>>(w.p2, (size_t)tn2 * T, w.tmax);

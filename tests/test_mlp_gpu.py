@@ -91,6 +91,30 @@ def test_mlp_bias_vs_oracle(ext, gpu):
     _compare_mlp(_np(out).reshape(T, dm), _np(osc), ref, rsc, "bias")
 
 
+# More than 512 rows, at most 128 tiles of 256 x 256 and no few-token path: both
+# GEMMs run 128 x 128 tiles (gemm_i8_mid_kernel).  (2048, 1024, 4096): interior tiles;
+# (1000, 528, 1040) and (777, 1040, 1552): ragged rows and columns, K not a multiple of
+# 128 (the zero-filled operand path and the guarded epilogue).
+@pytest.mark.parametrize("T,dm,dff", [(2048, 1024, 4096), (1000, 528, 1040), (777, 1040, 1552)])
+def test_mlp_mid_tiles_vs_oracle(ext, gpu, T, dm, dff):
+    c, n = _mlp_case(T, dm, dff, seed=T + 3 * dff, gpu=gpu)
+    bias = torch.randn(dff, generator=torch.Generator().manual_seed(T)) * 0.5
+    out, osc = ext.int8_mlp_forward_per_channel_bias(c["x"], c["W1"], c["W2"], c["sx"],
+                                                     c["sW1"], c["sW2"], bias.to(gpu))
+    torch.cuda.synchronize()
+    ref, rsc = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                             n["sW2"], bias1=bias.numpy(), gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out).reshape(T, dm), _np(osc), ref, rsc, f"mid T{T} dm{dm} dff{dff}")
+    # per-tensor output scale: the max over every 128-column partial
+    out_t, osc_t = capi.mlp_forward(c["x"].reshape(T, dm), c["W1"], c["W2"], c["sx"], c["sW1"],
+                                    c["sW2"], flags=capi.MLP_OUT_PER_TENSOR)
+    torch.cuda.synchronize()
+    ref_t, rsc_t = O.mlp_forward(n["x"].reshape(T, dm), n["W1"], n["W2"], n["sx"], n["sW1"],
+                                 n["sW2"], per_token_out=False, gemm=oracle_c.gemm_i8_i32)
+    _compare_mlp(_np(out_t), float(_np(osc_t).reshape(-1)[0]), ref_t, rsc_t,
+                 f"mid per-tensor T{T}")
+
+
 # Small GEMMs (M N K <= 2^31, K % 512 == 0) take the skinny path (32 x 32 tiles, K split
 # over the waves of a block): 1, 33 (a partial row tile), 64, 128, 200, 256, 300 rows.
 # K not a multiple of 512 takes split-K (128 x 128 tiles, K split over blocks, int32
