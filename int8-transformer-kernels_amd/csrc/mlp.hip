@@ -379,33 +379,48 @@ __device__ __forceinline__ void mid_mainloop(v16i (&acc)[kMidT][kMidT],
             *reinterpret_cast<int4*>(stage + kMidAStage + row * LDS_STRIDE + kc) = vb;
         }
     };
+    // fragments of k-slice s of a stage: rows (l % 32) of the wave's two 32-row
+    // blocks of A and of Bt, 16-byte half (l / 32)
+    auto read = [&](v4i (&a)[kMidT], v4i (&b)[kMidT], const char* stage, int s) {
+#pragma unroll
+        for (int i = 0; i < kMidT; ++i)
+            a[i] = *reinterpret_cast<const v4i*>(stage + a_off + i * 32 * LDS_STRIDE + s * 32);
+#pragma unroll
+        for (int j = 0; j < kMidT; ++j)
+            b[j] = *reinterpret_cast<const v4i*>(stage + b_off + j * 32 * LDS_STRIDE + s * 32);
+    };
+    auto mma = [&](const v4i (&a)[kMidT], const v4i (&b)[kMidT]) {
+#pragma unroll
+        for (int i = 0; i < kMidT; ++i)
+#pragma unroll
+            for (int j = 0; j < kMidT; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
     load(0);
     store(lds, 0);
     if (nk > 1) load(BK);
     __syncthreads();
+    v4i a[2][kMidT], b[2][kMidT];
+    read(a[0], b[0], lds, 0);
     // Step kt reads buffer kt & 1 and writes buffer (kt + 1) & 1, whose last
-    // reads (step kt - 1) finished before that step's barrier.
+    // reads (step kt - 1) finished before that step's barrier.  The fragments
+    // of slice 3 are in registers before the barrier, so its MFMAs run after
+    // it, while the reads of the next stage's slice 0 are in flight.
     for (int kt = 0; kt < nk; ++kt) {
         const char* cur = lds + (kt & 1) * kMidStage;
-#pragma unroll
-        for (int s = 0; s < BK / 32; ++s) {
-            v4i a[kMidT], b[kMidT];
-#pragma unroll
-            for (int i = 0; i < kMidT; ++i)
-                a[i] = *reinterpret_cast<const v4i*>(cur + a_off + i * 32 * LDS_STRIDE + s * 32);
-#pragma unroll
-            for (int j = 0; j < kMidT; ++j)
-                b[j] = *reinterpret_cast<const v4i*>(cur + b_off + j * 32 * LDS_STRIDE + s * 32);
-#pragma unroll
-            for (int i = 0; i < kMidT; ++i)
-#pragma unroll
-                for (int j = 0; j < kMidT; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0,
-                                                                      0);
-        }
-        if (kt + 1 < nk) store(lds + ((kt + 1) & 1) * kMidStage, (kt + 1) * BK);
+        char* nxt = lds + ((kt + 1) & 1) * kMidStage;
+        read(a[1], b[1], cur, 1);
+        mma(a[0], b[0]);
+        read(a[0], b[0], cur, 2);
+        mma(a[1], b[1]);
+        read(a[1], b[1], cur, 3);
+        mma(a[0], b[0]);
+        if (kt + 1 < nk) store(nxt, (kt + 1) * BK);
         if (kt + 2 < nk) load((kt + 2) * BK);
         __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 1 < nk) read(a[0], b[0], nxt, 0);
+        mma(a[1], b[1]);
     }
 }
 
