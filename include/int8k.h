@@ -65,6 +65,10 @@ const char* int8k_last_error(void);
 /* the split count automatically (sized for 256 CUs); a positive value       */
 /* forces that many KV chunks per (b,h) (clamped to what S allows) — the     */
 /* result is independent of it up to fp32 rounding.                          */
+/*                                                                          */
+/* The workspace holds split partials.  Plans of at most 16 chunks per (b,h) */
+/* merge their chunks on chip and need none: the query returns 0 and the    */
+/* call accepts a null workspace for them.                                  */
 /* ------------------------------------------------------------------------ */
 size_t int8k_decode_attention_workspace_bytes(int BH, int S, int head_dim, int nsplit);
 
@@ -93,7 +97,9 @@ int int8k_decode_attention_num_splits(int BH, int S, int head_dim, int nsplit);
  * the library holds, INT8K_DECODE_NOALLOC_SCRATCH_BYTES per GPU, from the
  * library's load until the process ends.  A call whose
  * int8k_decode_attention_workspace_bytes() exceeds that size returns
- * INT8K_ERR_WORKSPACE (int8k_last_error() says why) before touching the GPU.
+ * INT8K_ERR_WORKSPACE (int8k_last_error() says why) before touching the GPU;
+ * plans that merge their chunks on chip need no scratch and are never
+ * rejected for size.
  * All calls on one GPU share its array: calls that overlap on one GPU (other
  * streams, other threads) race and must be serialised by the caller.  Same
  * arguments, results and alignment as int8k_decode_attention_forward. */

@@ -1070,10 +1070,17 @@ extern "C" int int8k_decode_attention_num_splits(int BH, int S, int head_dim, in
     return plan_splits(BH, S, head_dim, nsplit).nsplit;
 }
 
+// Workspace a contiguous-cache decode with this plan needs: none when the chunks
+// of each (b,h) merge on chip (decode_block_kernel writes no partials), else
+// the split kernel's m, l and acc[D] per unit.
+static size_t decode_partial_bytes(const SplitPlan& plan, long long BH, int D) {
+    if (plan.nsplit <= kMaxBlockSplits && use_block_kernel()) return 0;
+    return carve(nullptr, BH * plan.nsplit, D).bytes;
+}
+
 extern "C" size_t int8k_decode_attention_workspace_bytes(int BH, int S, int head_dim, int nsplit) {
     if (BH <= 0 || S <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
-    const SplitPlan plan = plan_splits(BH, S, head_dim, nsplit);
-    return carve(nullptr, (long long)BH * plan.nsplit, head_dim).bytes;
+    return decode_partial_bytes(plan_splits(BH, S, head_dim, nsplit), BH, head_dim);
 }
 
 static bool out_ok(const DecodeOut& o) {
@@ -1097,9 +1104,13 @@ static int decode_impl(const int8_t* Q, const int8_t* K, const int8_t* V, const 
     const SplitPlan plan = plan_splits(BH, S, head_dim, nsplit);
     const long long units = (long long)BH * plan.nsplit;
     if (units >= (1LL << 26)) return INT8K_ERR_UNSUPPORTED;  // 64 work-items per unit, < 2^32
+    // the one-launch path reads no workspace: a null or short one is accepted there
+    if (decode_partial_bytes(plan, BH, head_dim) > 0) {
+        if (!workspace || workspace_bytes < carve(nullptr, units, head_dim).bytes)
+            return INT8K_ERR_WORKSPACE;
+        if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;
+    }
     const DecodeWorkspace w = carve(workspace, units, head_dim);
-    if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
-    if (!aligned_to(workspace, 16)) return INT8K_ERR_MISALIGNED;
     if (head_dim == 128)
         return launch_decode<128>(Q, K, V, out, scale_Q, scale_K, scale_V, BH, S, S_cap, plan,
                                   w, as_stream(stream));

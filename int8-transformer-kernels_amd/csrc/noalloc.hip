@@ -12,6 +12,9 @@
 // address of each GPU's copy comes from hipGetSymbolAddress, taken once per
 // device with that device current, and only that address is passed on.
 //
+// Only plans of more than 16 chunks per (b,h) run the split kernel and write
+// partials; the one-launch plans merge their chunks on chip, need no scratch
+// and are never refused for size (the workspace query returns 0 for them).
 // Every call on a GPU shares that GPU's array and leaves its partials there.
 // Nothing in it has to start at zero: each unit of the split kernel writes its
 // partial before the combine kernel reads it.  Two calls that overlap on one

@@ -69,9 +69,11 @@ constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
 // The V scales are applied once per staged tile, V^T = fp16(v * sV * 2^-E), and
 // the probabilities enter the PV MFMA as P = fp16(p * 2^E), so
 // P . V^T = sum_j p_j v_j sV_j as the reference's fp16(p * sV) . fp16(v)
-// (kernels/int8_attention.cu:530-572).  E >= 0 is the (b,h)'s exponent that
-// keeps 127 * max|sV| * 2^-E <= 32768 (0 for V from fp16 data), so V^T is
-// finite wherever the reference's P' is; E <= kMaxVExp.
+// (kernels/int8_attention.cu:530-572).  E >= 0 is chosen per block, from
+// max|sV| over the keys that block reads ([0, kv_end)), so that
+// 127 * max|sV| * 2^-E <= 32768 (0 for V from fp16 data) and V^T is finite
+// wherever the reference's P' is; E <= kMaxVExp.  Causal query tiles of one
+// (b,h) may use different E: each normalises with its own 2^E.
 constexpr int kMaxVExp = 11;
 
 // LDS position of key kk (0..63) of a tile inside a V^T row: keys

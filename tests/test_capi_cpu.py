@@ -46,9 +46,14 @@ def test_decode_argument_validation(capi):
     assert _decode_call(lib, D=256) == capi.INT8K_ERR_UNSUPPORTED
     assert _decode_call(lib, K=0x20001) == capi.INT8K_ERR_MISALIGNED
     assert _decode_call(lib, sK=0x60002) == capi.INT8K_ERR_MISALIGNED
-    need = capi.decode_workspace_bytes(4, 100, 128)
-    assert _decode_call(lib, ws_bytes=need - 1) == capi.INT8K_ERR_WORKSPACE
-    assert _decode_call(lib, ws=0) == capi.INT8K_ERR_WORKSPACE
+    # a forced 32-chunk plan runs the split kernel, whose partials need a workspace
+    need = capi.decode_workspace_bytes(4, 8192, 128, 32)
+    assert need > 0
+    assert _decode_call(lib, S=8192, nsplit=32, ws_bytes=need - 1) == capi.INT8K_ERR_WORKSPACE
+    assert _decode_call(lib, S=8192, nsplit=32, ws=0) == capi.INT8K_ERR_WORKSPACE
+    assert _decode_call(lib, S=8192, nsplit=32, ws=0x80008) == capi.INT8K_ERR_MISALIGNED
+    # plans merged on chip need none
+    assert capi.decode_workspace_bytes(4, 100, 128) == 0
 
 
 @pytest.mark.parametrize("BH,S,D", [(1, 1, 64), (12, 1024, 64), (1024, 8192, 128),
@@ -57,7 +62,10 @@ def test_decode_split_plan(capi, BH, S, D):
     ns = capi.decode_num_splits(BH, S, D)
     assert 1 <= ns <= S
     ws = capi.decode_workspace_bytes(BH, S, D)
-    assert ws >= BH * ns * (D + 2) * 4
+    if ns > 16:
+        assert ws >= BH * ns * (D + 2) * 4
+    else:
+        assert ws == 0  # the one-launch kernel merges the chunks on chip
     # forced split counts are honoured up to what S allows
     assert capi.decode_num_splits(BH, S, D, 1) == 1
     assert capi.decode_num_splits(BH, S, D, 10 ** 6) <= S
@@ -177,13 +185,15 @@ def test_quantized_attention_output_validation(capi):
         assert fwd(flags) == capi.INT8K_ERR_UNSUPPORTED
     for flags in (4, 8, -1):
         assert fwd(flags) == capi.INT8K_ERR_INVALID_ARGUMENT
+    # a forced 32-chunk plan: the split kernel, whose partials need a workspace
     dec = lambda q=0x40000, s=0x48000, ws_bytes=1 << 30: (  # noqa: E731
         lib.int8k_decode_attention_forward_quant(
             F(0x10000), F(0x20000), F(0x30000), F(q), F(s), F(0x50000), F(0x60000), F(0x70000),
-            4, 100, 128, 0, F(0x80000), ws_bytes, None))
+            4, 8192, 128, 32, F(0x80000), ws_bytes, None))
     assert dec(q=0) == capi.INT8K_ERR_INVALID_ARGUMENT
     assert dec(s=0x48001) == capi.INT8K_ERR_MISALIGNED
-    assert dec(ws_bytes=capi.decode_workspace_bytes(4, 100, 128) - 1) == capi.INT8K_ERR_WORKSPACE
+    assert dec(ws_bytes=capi.decode_workspace_bytes(4, 8192, 128, 32) - 1) == \
+        capi.INT8K_ERR_WORKSPACE
     assert lib.int8k_decode_attention_forward_cache_quant(
         F(0x10000), F(0x20000), F(0x30000), F(0x40000), F(0), F(0x50000), F(0x60000),
         F(0x70000), 4, 100, 90, 128, 0, F(0x80000), 1 << 30, None) == \
