@@ -546,7 +546,9 @@ def measure_mlp(args, dev, stream, cpu_budget=None):
     ops = 4 * T * dm * dff
     times = {}
     for name, flags, w1, w2 in (("prepacked", capi.MLP_WEIGHTS_PREPACKED, W1T, W2T),
-                                ("unpacked", 0, c["W1"], c["W2"])):
+                                ("unpacked", 0, c["W1"], c["W2"]),
+                                ("separate", capi.MLP_WEIGHTS_PREPACKED |
+                                 capi.MLP_SEPARATE_REQUANT, W1T, W2T)):
         ws = torch.empty(capi.mlp_workspace_bytes(T, dm, dff, flags), dtype=torch.uint8,
                          device=dev)
 
@@ -579,6 +581,8 @@ def measure_mlp(args, dev, stream, cpu_budget=None):
                      "W, prepacked weights",
          "us": round(ms * 1e3, 2), "TOPS": round(tops, 1), "windows_ms": windows,
          "unpacked_us": round(times["unpacked"][0] * 1e3, 2),
+         "separate_requant_us": round(times["separate"][0] * 1e3, 2),
+         "sync_timeouts": capi.mlp_sync_timeouts(),
          "parity": {"rows_checked": len(rows), "max_lsb": int(diff.max()),
                     "frac_off_by_one": round(float((diff != 0).mean()), 5)},
          "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,

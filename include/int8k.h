@@ -253,8 +253,24 @@ int int8k_attention_forward_quant(
 /* ------------------------------------------------------------------------ */
 #define INT8K_MLP_WEIGHTS_PREPACKED 1
 #define INT8K_MLP_OUT_PER_TENSOR 2
+/* Where a GEMM runs on the 256 x 256 tiled kernel (T * d_ff or T * d_model
+ * above 2^23, d_ff and d_model up to 32768), its epilogue finishes the
+ * per-token requantization: the tiles of a 256-row stripe exchange their row
+ * maxima through the workspace, and neither the fp16 hidden nor the fp16
+ * output reaches memory.  The codes are those of the separate pass (fp16 rows
+ * + requant), byte for byte.  This flag keeps the separate pass (no
+ * counterpart in the reference; for comparison and measurement). */
+#define INT8K_MLP_SEPARATE_REQUANT 4
 
 size_t int8k_mlp_workspace_bytes(int T, int d_model, int d_ff, int flags);
+
+/* Diagnostics of the fused requantization: *count receives how many tiles, on
+ * the current device since the library was loaded, stopped waiting for their
+ * stripe's row maxima (a bounded wait that gives up after ~0.67 s and then
+ * uses the maxima that have arrived).  It stays 0 when every tile of a stripe
+ * can be resident at once, which the launch order provides on MI355X.
+ * Synchronises with the device.  No counterpart in the reference. */
+int int8k_mlp_sync_timeouts(unsigned int* count);
 
 int int8k_mlp_forward(
     const int8_t* x, const int8_t* W1, const int8_t* W2, int8_t* out,

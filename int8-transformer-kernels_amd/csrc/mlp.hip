@@ -316,6 +316,253 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     }
 }
 
+// ------------------------------------------------------------ requant fused into the GEMM
+// gemm_i8_rq_kernel<EPI>: gemm_i8_kernel whose epilogue also finishes the
+// per-token requantization, so the fp16 rows never reach memory and no
+// requant pass runs.  The row max that a code needs spans every column tile
+// of the row's 256-row stripe, so the tiles of a stripe exchange it:
+//   1. each tile computes v (scales, bias, GELU) and fp16(v) from its live
+//      accumulators, keeps the fp16 pairs in registers and reduces the row
+//      maxima of |v| over its 256 columns (fp32, before rounding);
+//   2. it folds them into amax[row] (device-scope atomic max on the float
+//      bits: |v| >= 0 orders like the integers) and, once those atomics have
+//      completed, adds one to arrived[stripe];
+//   3. one lane waits until arrived[stripe] counts every tile of the stripe,
+//      reading the counter and then amax[row] with device-scope atomic loads
+//      (they bypass the XCD's L2, so no cache flush is needed);
+//   4. code = rint(clamp(f32(fp16(v)) * (127 / max(amax, 1e-8)))), the
+//      expression of requant_rows_kernel, so the codes are that pass's codes
+//      byte for byte; the stripe's column-0 tile writes the row scales
+//      max(amax, 1e-8) / 127.
+// The wait needs every tile of a stripe resident at once.  Blocks map to
+// tiles in groups of stripes; inside a group each XCD (block id % 8) takes a
+// panel of stripes x columns and walks it stripe by stripe, so a stripe's
+// tiles come right after the tiles of earlier stripes in every XCD's
+// dispatch order: with blocks dispatched in id order, a stripe is waited on
+// only once all its tiles are resident or done.  The host takes this path
+// only when a stripe has at most kRqMaxStripeTiles tiles (half the CUs).  The
+// wait is bounded in time nevertheless (every wave exits); a wait that gives
+// up counts in g_rq_timeouts (int8k_mlp_sync_timeouts) and the tile then
+// uses the maxima that have arrived.
+constexpr int kRqMaxStripeTiles = 128;
+constexpr unsigned long long kRqWaitTicks = 1ull << 26;  // s_memrealtime (100 MHz): ~0.67 s
+
+__device__ unsigned int g_rq_timeouts;
+
+struct RqParams {
+    int8_t* q;           // codes [M][ldq]
+    int ldq;
+    float* scales;       // [M] row scale max(amax, 1e-8) / 127
+    uint32_t* amax;      // [M] max |v| of the row as float bits; zero before the launch
+    uint32_t* arrived;   // [tiles_m] tiles of the stripe that published; zero before the launch
+    int gs;              // stripes per group
+    int xm, xn;          // XCD panel grid of a group (xm * xn == 8); xn == 0: stripe-major order
+};
+
+// Block id -> (stripe, column tile); see the dispatch-order note above.
+__device__ __forceinline__ void rq_tile_coords(int bid, int tiles_m, int tiles_n,
+                                               const RqParams& rq, int& tm, int& tn) {
+    const int per_group = rq.gs * tiles_n;
+    const int g = bid / per_group, b = bid - g * per_group;
+    const int s0 = g * rq.gs;
+    if (rq.xn > 0 && s0 + rq.gs <= tiles_m) {
+        const int x = b % kNumXcd, l = b / kNumXcd;
+        const int pn = tiles_n / rq.xn, pm = rq.gs / rq.xm;
+        tm = s0 + (x % rq.xm) * pm + l / pn;
+        tn = (x / rq.xm) * pn + l % pn;
+    } else {
+        tm = s0 + b / tiles_n;
+        tn = b % tiles_n;
+    }
+}
+
+// The code of one fp16 value (low 16 bits of `bits`) with inverse scale inv, as
+// the low byte of a float's bits: clamp(h * inv) + 1.5 * 2^23 rounds half to
+// even onto the integer grid (|x| <= 128), like rint in requant_rows_kernel.
+__device__ __forceinline__ uint32_t rq_code_bits(uint32_t bits, float inv) {
+#pragma clang fp contract(off)
+    const float f = __half2float(__ushort_as_half((uint16_t)(bits & 0xffff))) * inv;
+    return __float_as_uint(fminf(fmaxf(f, -128.f), 127.f) + 12582912.0f);
+}
+
+// 4 x 4 byte transpose across each aligned group of 4 lanes: lane m of the group
+// holds byte k = (row k, column m) and ends with byte k = (row m, column k).
+__device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t d, int lane) {
+    const uint32_t p2 = __builtin_amdgcn_mov_dpp(d, 0x4E, 0xF, 0xF, true);  // lane ^ 2
+    d = __builtin_amdgcn_perm(p2, d, (lane & 2) ? 0x03020706u : 0x05040100u);
+    const uint32_t p1 = __builtin_amdgcn_mov_dpp(d, 0xB1, 0xF, 0xF, true);  // lane ^ 1
+    return __builtin_amdgcn_perm(p1, d, (lane & 1) ? 0x03070105u : 0x06020400u);
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const EpiParams& p,
+                                            const RqParams& rq, int M, int N, int m0, int n0,
+                                            int tm, int tn, int tiles_n, float pre_sa,
+                                            float pre_sb, float pre_b, char* lds) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int* rowmax = reinterpret_cast<int*>(lds);  // [2][BM]: per column half of the waves
+    float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
+    float* esb = esa + BM;
+    float* ebias = esb + BM;
+    esa[t] = pre_sa;
+    esb[t] = pre_sb;
+    ebias[t] = pre_b;
+    __syncthreads();
+    // 1. values, their fp16 pairs (rows r, r+1 of the lane's column) and row maxima
+    uint32_t h[TM][TN][8];
+    float sbv[TN], biv[TN];
+    bool cok[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int cl = wn * WN + j * 32 + (lane & 31);
+        sbv[j] = esb[cl];
+        biv[j] = ebias[cl];
+        cok[j] = n0 + cl < N;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        float sav[16], rmax[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 s4 =
+                *reinterpret_cast<const float4*>(esa + wm * WM + i * 32 + q * 8 + (lane >> 5) * 4);
+            sav[4 * q] = s4.x, sav[4 * q + 1] = s4.y, sav[4 * q + 2] = s4.z, sav[4 * q + 3] = s4.w;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = static_cast<float>(acc[i][j][r]) * sav[r] * sbv[j];
+            if constexpr (EPI == EPI_GELU_F16) {
+                float e[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = v[r] + biv[j];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) e[r] = gelu_exponent(v[r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) e[r] = fast_exp2(e[r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_rcpf(1.f + e[r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = v[r] * e[r];
+            }
+            // columns past N do not count (their accumulators are zero, v need not be)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) rmax[r] = fmaxf(rmax[r], cok[j] ? fabsf(v[r]) : 0.f);
+#pragma unroll
+            for (int r = 0; r < 16; r += 2)
+                h[i][j][r >> 1] =
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){v[r], v[r + 1]}, h2));
+        }
+        tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
+    }
+    __syncthreads();
+    // 2. publish the tile's row maxima, then its arrival
+    const int row_t = m0 + t;
+    if (row_t < M) {
+        const uint32_t m = (uint32_t)max(rowmax[t], rowmax[BM + t]);
+        __hip_atomic_fetch_max(rq.amax + row_t, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the atomics have completed (vmcnt(0)) before any lane of the block goes on
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+    __syncthreads();
+    if (t == 0) {
+        __hip_atomic_fetch_add(rq.arrived + tm, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // 3. wait for the stripe's other tiles
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(rq.arrived + tm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+               (uint32_t)tiles_n) {
+            __builtin_amdgcn_s_sleep(2);
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kRqWaitTicks) {
+                __hip_atomic_fetch_add(&g_rq_timeouts, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // the rows' inverse scales replace the row scales in LDS (last read before the barrier above)
+    {
+        const uint32_t bits = __hip_atomic_load(rq.amax + min(row_t, M - 1), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        const float amax = fmaxf(__uint_as_float(bits), 1e-8f);
+        esa[t] = 127.f / amax;
+        if (tn == 0 && row_t < M) rq.scales[row_t] = amax / 127.f;
+    }
+    __syncthreads();
+    // 4. codes: per (i, q) a lane holds rows base + 0..3 of its column for each j; packed into
+    // a dword and transposed across the 4 lanes of 4 consecutive columns, each lane stores
+    // row base + lane % 4, columns 4 * (lane % 32 / 4) .. + 3 of column tile j
+    const bool interior = m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int rl = wm * WM + i * 32 + q * 8 + (lane >> 5) * 4;  // first of the 4 rows
+            const float4 inv4 = *reinterpret_cast<const float4*>(esa + rl);
+            uint32_t d[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t w0 = h[i][j][2 * q], w1 = h[i][j][2 * q + 1];
+                const uint32_t c0 = rq_code_bits(w0, inv4.x), c1 = rq_code_bits(w0 >> 16, inv4.y);
+                const uint32_t c2 = rq_code_bits(w1, inv4.z), c3 = rq_code_bits(w1 >> 16, inv4.w);
+                const uint32_t col4 = __builtin_amdgcn_perm(c1, c0, 0x0c0c0400u) |
+                                      __builtin_amdgcn_perm(c3, c2, 0x04000c0cu);
+                d[j] = quad_transpose_bytes(col4, lane);
+            }
+            const int row = m0 + rl + (lane & 3);
+            const int cl = wn * WN + 4 * ((lane & 31) >> 2);
+            int8_t* dst = rq.q + (size_t)row * rq.ldq + n0 + cl;
+            if (interior) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) *reinterpret_cast<uint32_t*>(dst + j * 32) = d[j];
+            } else if (row < M) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        if (n0 + cl + j * 32 + b < N) dst[j * 32 + b] = (int8_t)(d[j] >> (8 * b));
+            }
+        }
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_i8_rq_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int M, int N, int K,
+    int tiles_m, int tiles_n, EpiParams p, RqParams rq) {
+    static_assert(EPI == EPI_GELU_F16 || EPI == EPI_F16, "requantizing epilogues only");
+    extern __shared__ __align__(16) char lds[];
+    int tm, tn;
+    rq_tile_coords(blockIdx.x, tiles_m, tiles_n, rq, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x;
+    const float pre_sa = p.sa[(size_t)min(m0 + t, M - 1) * p.sa_stride];
+    const float pre_sb = p.sb[(size_t)min(n0 + t, N - 1) * p.sb_stride];
+    const float pre_b = p.bias != nullptr ? p.bias[min(n0 + t, N - 1)] : 0.f;
+    v16i acc[TM][TN];
+    if (m0 + BM <= M && n0 + BN <= N && K % BK == 0)
+        mainloop<false>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
+    else
+        mainloop<true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
+    epilogue_rq<EPI>(acc, p, rq, M, N, m0, n0, tm, tn, tiles_n, pre_sa, pre_sb, pre_b, lds);
+}
+
+// Zeroes n dwords (the fused requant's amax and arrival counters) before the GEMMs.
+__global__ __launch_bounds__(256) void rq_clear_kernel(uint32_t* __restrict__ p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
 // ------------------------------------------------------------ mid-size grids
 // gemm_i8_mid_kernel<EPI>: 128 x 128 output tiles for GEMMs whose 256 x 256
 // grid leaves CUs idle (T = 4096 at d_model 1024: GEMM2 has 16 x 4 big tiles
@@ -1011,6 +1258,52 @@ int launch_gemm_mid(const int8_t* A, const int8_t* Bt, int M, int N, int K, cons
     return check_launch("gemm_i8_mid_kernel");
 }
 
+// Tile order of a fused-requant GEMM: per group of stripes, each XCD takes a panel
+// of pm stripes x pn column tiles (about 32 tiles, one round of its CUs) with
+// the smallest pm + pn, which is the operand bytes its L2 holds per K-step.  A
+// stripe's pn tiles on one XCD must be resident together, so pn stays at most
+// kRqMaxPanelCols (half an XCD's 32 CUs); shapes with no such panel take the
+// stripe-major order, which spreads a stripe over the XCDs round-robin.
+constexpr int kRqMaxPanelCols = 16;
+
+RqParams rq_layout(int tiles_m, int tiles_n) {
+    RqParams r{};
+    r.gs = 1;
+    r.xm = 1;
+    r.xn = 0;
+    int best = 1 << 30;
+    for (int xn = 8; xn >= 1; xn >>= 1) {
+        if (tiles_n % xn != 0) continue;
+        const int pn = tiles_n / xn, xm = kNumXcd / xn;
+        const int pm = std::max(1, 32 / pn);
+        if (pn <= kRqMaxPanelCols && pm + pn < best && pm * xm <= std::max(tiles_m, xm)) {
+            best = pm + pn;
+            r.xn = xn;
+            r.xm = xm;
+            r.gs = pm * xm;
+        }
+    }
+    return r;
+}
+
+// A GEMM with the per-token requantization in its epilogue: codes q [M][N] and
+// row scales; amax [M] and arrived [tiles_m] must be zero.
+template <int EPI>
+int launch_gemm_rq(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
+                   int8_t* q, float* scales, uint32_t* amax, uint32_t* arrived,
+                   hipStream_t stream) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    RqParams rq = rq_layout(tiles_m, tiles_n);
+    rq.q = q;
+    rq.ldq = N;
+    rq.scales = scales;
+    rq.amax = amax;
+    rq.arrived = arrived;
+    gemm_i8_rq_kernel<EPI><<<tiles_m * tiles_n, kThreads, kEpiLdsBytes, stream>>>(
+        A, Bt, M, N, K, tiles_m, tiles_n, p, rq);
+    return check_launch("gemm_i8_rq_kernel");
+}
+
 int launch_transpose(const int8_t* src, int8_t* dst, int R, int C, hipStream_t stream) {
     const dim3 grid((C + kTrTile - 1) / kTrTile, (R + kTrTile - 1) / kTrTile);
     const int vec_ok = R % 16 == 0 && C % 16 == 0 && aligned_to(src, 16) && aligned_to(dst, 16);
@@ -1018,22 +1311,62 @@ int launch_transpose(const int8_t* src, int8_t* dst, int R, int C, hipStream_t s
     return check_launch("transpose_i8_kernel");
 }
 
+// Whether the tiled GEMM2 reads the fp16 hidden with on-load quantization
+// (gemm_i8_a16_kernel) instead of the int8 hidden.  Both give the same bytes;
+// the on-load path was measured slower on MI355X at the BASELINE shape (it
+// doubles GEMM2's A bytes and adds ~3 VALU ops per element to a loop that has
+// no VALU slack) and needs GEMM1's fp16 hidden, so it also turns off GEMM1's
+// fused requantization.  INT8K_MLP_GEMM2_FP16_HIDDEN=1 selects it (read on
+// every call and workspace query).
+bool gemm2_reads_fp16_hidden() {
+    const char* e = std::getenv("INT8K_MLP_GEMM2_FP16_HIDDEN");
+    return e != nullptr && e[0] == '1';
+}
+
+// Which GEMMs of an MLP call requantize in their epilogue (gemm_i8_rq_kernel):
+// those on the 256 x 256 tiled kernel with at most kRqMaxStripeTiles column
+// tiles per stripe; GEMM2 only for the per-token output.  The flag
+// INT8K_MLP_SEPARATE_REQUANT (or INT8K_MLP_FUSED_REQUANT=0 in the environment,
+// read once) keeps both on the fp16 output + requant_rows_kernel path.
+struct RqPlan {
+    bool g1, g2;
+};
+
+inline bool rq_fusable(int M, int N, int K) {
+    if (use_skinny(M, N, K) || splitk_plan(M, N, K).use || use_mid(M, N, K)) return false;
+    return (N + BN - 1) / BN <= kRqMaxStripeTiles;
+}
+
+RqPlan rq_plan(int T, int dm, int dff, int flags) {
+    static const bool env_on = [] {
+        const char* e = std::getenv("INT8K_MLP_FUSED_REQUANT");
+        return !(e != nullptr && e[0] == '0');
+    }();
+    const bool on = env_on && (flags & INT8K_MLP_SEPARATE_REQUANT) == 0;
+    RqPlan pl;
+    pl.g1 = on && !gemm2_reads_fp16_hidden() && rq_fusable(T, dff, dm);
+    pl.g2 = on && (flags & INT8K_MLP_OUT_PER_TENSOR) == 0 && rq_fusable(T, dm, dff);
+    return pl;
+}
+
 // Workspace layout of one MLP call (all offsets 256-byte aligned).
 struct MlpWorkspace {
     int8_t* w1t;      // [d_ff][d_model]  (absent when prepacked)
     int8_t* w2t;      // [d_model][d_ff]
-    uint16_t* h16;    // [T][d_ff]
+    uint16_t* h16;    // [T][d_ff]          (absent when GEMM1 requantizes)
     int8_t* hq;       // [T][d_ff]
     float* sh;        // [T]
-    float* p1;        // [tiles_n1][T]
-    uint16_t* o16;    // [T][d_model]
-    float* p2;        // [tiles_n2][T]
+    float* p1;        // [tiles_n1][T]      (absent when GEMM1 requantizes)
+    uint16_t* o16;    // [T][d_model]       (absent when GEMM2 requantizes)
+    float* p2;        // [tiles_n2][T]      (absent when GEMM2 requantizes)
     float* tmax;      // [1]
+    uint32_t* sync;   // fused requant: amax1 [T], amax2 [T], arrived1 [tiles_m], arrived2 [tiles_m]
+    int sync_words;
     int32_t* part;    // split-K partials (the larger GEMM's), when a GEMM runs split-K
     size_t bytes;
 };
 
-MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
+MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked, const RqPlan& rp) {
     char* p = static_cast<char*>(base);
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -1045,29 +1378,21 @@ MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked) {
     const size_t wbytes = prepacked ? 0 : (size_t)dm * dff;
     w.w1t = reinterpret_cast<int8_t*>(take(wbytes));
     w.w2t = reinterpret_cast<int8_t*>(take(wbytes));
-    w.h16 = reinterpret_cast<uint16_t*>(take((size_t)T * dff * 2));
+    w.h16 = reinterpret_cast<uint16_t*>(take(rp.g1 ? 0 : (size_t)T * dff * 2));
     w.hq = reinterpret_cast<int8_t*>(take((size_t)T * dff));
     w.sh = reinterpret_cast<float*>(take((size_t)T * 4));
-    w.p1 = reinterpret_cast<float*>(take((size_t)epi_tiles(T, dff, dm) * T * 4));
-    w.o16 = reinterpret_cast<uint16_t*>(take((size_t)T * dm * 2));
-    w.p2 = reinterpret_cast<float*>(take((size_t)epi_tiles(T, dm, dff) * T * 4));
+    w.p1 = reinterpret_cast<float*>(take(rp.g1 ? 0 : (size_t)epi_tiles(T, dff, dm) * T * 4));
+    w.o16 = reinterpret_cast<uint16_t*>(take(rp.g2 ? 0 : (size_t)T * dm * 2));
+    w.p2 = reinterpret_cast<float*>(take(rp.g2 ? 0 : (size_t)epi_tiles(T, dm, dff) * T * 4));
     w.tmax = reinterpret_cast<float*>(take(4));
+    const int tiles_m = (T + BM - 1) / BM;
+    w.sync_words = (rp.g1 || rp.g2) ? 2 * T + 2 * tiles_m : 0;
+    w.sync = reinterpret_cast<uint32_t*>(take((size_t)w.sync_words * 4));
     const size_t part1 = use_skinny(T, dff, dm) ? 0 : splitk_partial_bytes(T, dff, dm);
     const size_t part2 = use_skinny(T, dm, dff) ? 0 : splitk_partial_bytes(T, dm, dff);
     w.part = reinterpret_cast<int32_t*>(take(std::max(part1, part2)));
     w.bytes = off;
     return w;
-}
-
-// Whether the tiled GEMM2 reads the fp16 hidden with on-load quantization
-// (gemm_i8_a16_kernel) instead of the int8 hidden of requant_rows_kernel.
-// Both give the same bytes; the default is the separate pass, measured faster
-// on MI355X at the BASELINE shape (the on-load path doubles GEMM2's A bytes
-// and adds ~3 VALU ops per element to a loop that has no VALU slack).
-// INT8K_MLP_GEMM2_FP16_HIDDEN=1 selects the on-load path, read on every call.
-bool gemm2_reads_fp16_hidden() {
-    const char* e = std::getenv("INT8K_MLP_GEMM2_FP16_HIDDEN");
-    return e != nullptr && e[0] == '1';
 }
 
 PerDeviceOnce lds_once;
@@ -1081,6 +1406,12 @@ int configure_lds() {
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_rq_kernel<EPI_GELU_F16>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)gemm_i8_rq_kernel<EPI_F16>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)gemm_i8_a16_kernel,
@@ -1129,7 +1460,21 @@ extern "C" int int8k_transpose_int8_weights(const int8_t* W1, const int8_t* W2, 
 
 extern "C" size_t int8k_mlp_workspace_bytes(int T, int d_model, int d_ff, int flags) {
     if (T <= 0 || d_model <= 0 || d_ff <= 0) return 0;
-    return carve_mlp(nullptr, T, d_model, d_ff, (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0).bytes;
+    return carve_mlp(nullptr, T, d_model, d_ff, (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0,
+                     rq_plan(T, d_model, d_ff, flags))
+        .bytes;
+}
+
+extern "C" int int8k_mlp_sync_timeouts(unsigned int* count) {
+    clear_last_error();
+    if (!count) return INT8K_ERR_INVALID_ARGUMENT;
+    const hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_rq_timeouts), sizeof(unsigned int),
+                                             0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        set_last_error("hipMemcpyFromSymbol(g_rq_timeouts)", e);
+        return INT8K_ERR_HIP;
+    }
+    return INT8K_OK;
 }
 
 extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t* W2, int8_t* out,
@@ -1145,7 +1490,8 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     if ((n_scale_x != 1 && n_scale_x != T) || (n_scale_W1 != 1 && n_scale_W1 != d_ff) ||
         (n_scale_W2 != 1 && n_scale_W2 != d_model))
         return INT8K_ERR_INVALID_ARGUMENT;
-    if ((flags & ~(INT8K_MLP_WEIGHTS_PREPACKED | INT8K_MLP_OUT_PER_TENSOR)) != 0)
+    if ((flags & ~(INT8K_MLP_WEIGHTS_PREPACKED | INT8K_MLP_OUT_PER_TENSOR |
+                   INT8K_MLP_SEPARATE_REQUANT)) != 0)
         return INT8K_ERR_INVALID_ARGUMENT;
     if (d_model % 16 != 0 || d_ff % 16 != 0) return INT8K_ERR_UNSUPPORTED;
     if (!aligned_to(x, 16) || !aligned_to(W1, 16) || !aligned_to(W2, 16) || !aligned_to(out, 4) ||
@@ -1154,12 +1500,23 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
         return INT8K_ERR_MISALIGNED;
     const bool prepacked = (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0;
     const bool per_tensor_out = (flags & INT8K_MLP_OUT_PER_TENSOR) != 0;
-    const MlpWorkspace w = carve_mlp(workspace, T, d_model, d_ff, prepacked);
+    const RqPlan rp = rq_plan(T, d_model, d_ff, flags);
+    const MlpWorkspace w = carve_mlp(workspace, T, d_model, d_ff, prepacked, rp);
     if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
     if (!aligned_to(workspace, 256)) return INT8K_ERR_MISALIGNED;
     int st = configure_lds();
     if (st != INT8K_OK) return st;
     hipStream_t s = as_stream(stream);
+    const int tiles_m = (T + BM - 1) / BM;
+    uint32_t* amax1 = w.sync;
+    uint32_t* amax2 = w.sync + T;
+    uint32_t* arrived1 = w.sync + 2 * T;
+    uint32_t* arrived2 = arrived1 + tiles_m;
+    if (w.sync_words > 0) {
+        rq_clear_kernel<<<std::min(64, (w.sync_words + 255) / 256), 256, 0, s>>>(w.sync,
+                                                                               w.sync_words);
+        if ((st = check_launch("rq_clear_kernel")) != INT8K_OK) return st;
+    }
 
     const int8_t* W1t = W1;
     const int8_t* W2t = W2;
@@ -1180,7 +1537,10 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p1.bias = bias1;
     p1.pmax = w.p1;
     const SplitKPlan sk1 = splitk_plan(T, d_ff, d_model);
-    if (use_skinny(T, d_ff, d_model))
+    if (rp.g1)
+        st = launch_gemm_rq<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, w.hq, w.sh, amax1,
+                                          arrived1, s);
+    else if (use_skinny(T, d_ff, d_model))
         st = launch_gemm_skinny<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     else if (sk1.use)
         st = launch_gemm_splitk<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, sk1, w.part, p1, s);
@@ -1202,7 +1562,17 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     const SplitKPlan sk2 = splitk_plan(T, d_model, d_ff);
     const bool skinny2 = use_skinny(T, d_model, d_ff);
     // the on-load path has 256 x 256 tiles on every grid it runs
-    const bool a16 = !skinny2 && !sk2.use && gemm2_reads_fp16_hidden();
+    const bool a16 = !rp.g1 && !skinny2 && !sk2.use && gemm2_reads_fp16_hidden();
+    if (!rp.g1 && !a16) {
+        // per-token requant of the hidden (one absmax partial per row and 256-column
+        // tile, or per 32-column block of the skinny path)
+        if ((st = launch_requant(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T, d_ff,
+                                 s)) != INT8K_OK)
+            return st;
+    }
+    if (rp.g2)
+        return launch_gemm_rq<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, out, out_scale, amax2,
+                                       arrived2, s);
     if (a16) {
         // the tiled GEMM2 reads the fp16 hidden and quantizes it per row on load
         const int tiles_m = (T + BM - 1) / BM, tiles_n = (d_model + BN - 1) / BN;
@@ -1210,11 +1580,6 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
             w.h16, W2t, T, d_model, d_ff, tiles_m, tiles_n, w.p1, tn1, p2);
         if ((st = check_launch("gemm_i8_a16_kernel")) != INT8K_OK) return st;
     } else {
-        // per-token requant of the hidden (one absmax partial per row and 256-column
-        // tile, or per 32-column block of the skinny path)
-        if ((st = launch_requant(w.h16, d_ff, w.p1, tn1, nullptr, w.hq, d_ff, w.sh, T, d_ff,
-                                 s)) != INT8K_OK)
-            return st;
         if (skinny2)
             st = launch_gemm_skinny<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
         else if (sk2.use)

@@ -62,12 +62,14 @@ _SIGNATURES = {
     "int8k_decode_attention_forward_cache_quant": (_I, [_P] * 8 + [_I] * 5 + [_P, _SZ, _P]),
     "int8k_decode_attention_forward_paged_quant": (_I, [_P] * 10 + [_I] * 8 + [_P, _SZ, _P]),
     "int8k_decode_attention_forward_noalloc": (_I, [_P] * 7 + [_I] * 4 + [_P]),
+    "int8k_mlp_sync_timeouts": (_I, [ctypes.POINTER(ctypes.c_uint)]),
 }
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 
 MLP_WEIGHTS_PREPACKED = 1
 MLP_OUT_PER_TENSOR = 2
+MLP_SEPARATE_REQUANT = 4
 
 _lib = None
 
@@ -210,6 +212,14 @@ def transpose_int8_weights(W1, W2):
 
 def mlp_workspace_bytes(T, d_model, d_ff, flags=0):
     return load().int8k_mlp_workspace_bytes(T, d_model, d_ff, flags)
+
+
+def mlp_sync_timeouts() -> int:
+    """Tiles whose wait for their stripe's row maxima gave up (fused requantization), on the
+    current device since the library was loaded; synchronises with the device."""
+    n = ctypes.c_uint(0)
+    check("int8k_mlp_sync_timeouts", load().int8k_mlp_sync_timeouts(ctypes.byref(n)))
+    return int(n.value)
 
 
 def mlp_forward(x, W1, W2, sx, sW1, sW2, bias1=None, flags=0, out=None, out_scale=None,
