@@ -128,13 +128,23 @@ __device__ __forceinline__ void read_slice(v4i (&a)[TM], v4i (&b)[TN], const cha
         b[j] = *reinterpret_cast<const v4i*>(stage + b_off + j * 32 * LDS_STRIDE + slice * 32);
 }
 
+// One 32x32x32 MFMA of tile (i, j).  SWAP computes the tile transposed (B . A^T):
+// the same sums, with a lane holding one row and 16 columns instead of one
+// column and 16 rows (see acc_row).
+template <bool SWAP>
+__device__ __forceinline__ v16i mfma_ab(const v4i& a, const v4i& b, const v16i& c) {
+    if constexpr (SWAP) return __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+template <bool SWAP = false>
 __device__ __forceinline__ void mfma_slice(v16i (&acc)[TM][TN], const v4i (&a)[TM],
                                            const v4i (&b)[TN]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = mfma_ab<SWAP>(a[i], b[j], acc[i][j]);
 }
 
 // Instruction classes for __builtin_amdgcn_sched_group_barrier.
@@ -166,7 +176,7 @@ __device__ __forceinline__ void sched_reads_mfma() {
 // Writing buffer (kt+1)&1 during step kt is safe: its last reads (step kt-1)
 // completed before step kt-1's barrier.  Past the end of K the loads clamp to
 // valid addresses and the writes land in the buffer nobody reads again.
-template <bool EDGE>
+template <bool EDGE, bool SWAP = false>
 __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __restrict__ A,
                                          const int8_t* __restrict__ Bt, int M, int N, int K,
                                          int lda, int ldb, int m0, int n0, char* lds) {
@@ -198,11 +208,11 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
         char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
         __builtin_amdgcn_sched_barrier(0);
         read_slice(a[1], b[1], cur, a_off, b_off, 1);
-        mfma_slice(acc, a[0], b[0]);
+        mfma_slice<SWAP>(acc, a[0], b[0]);
         sched_reads_mfma();
         __builtin_amdgcn_sched_barrier(0);
         read_slice(a[0], b[0], cur, a_off, b_off, 2);
-        mfma_slice(acc, a[1], b[1]);
+        mfma_slice<SWAP>(acc, a[1], b[1]);
         sched_reads_mfma();
         __builtin_amdgcn_sched_barrier(0);
         // slice 2, one group per MFMA: a fragment read of slice 3, a chunk
@@ -219,15 +229,14 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
                 store_chunk<EDGE>(f.b[g - 8], nxt + A_STAGE, N, K, n0, (kt + 1) * BK, g - 8);
                 f.b[g - 8] = load_chunk(Bt, N, K, ldb, n0, (kt + 2) * BK, g - 8);
             }
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = mfma_ab<SWAP>(a[0][i], b[0][j], acc[i][j]);
             __builtin_amdgcn_sched_barrier(0);
         }
         // slice 3: half of its MFMAs cover the LDS writes before the barrier,
         // the other half the reads of the next stage's slice 0 after it
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
-            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            acc[g >> 2][g & 3] = mfma_ab<SWAP>(a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3]);
             __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
@@ -235,8 +244,7 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
         for (int g = 8; g < 16; ++g) {
             if (g < 12) a[0][g - 8] = read_frag(nxt, a_off, g - 8, 0);
             else b[0][g - 12] = read_frag(nxt, b_off, g - 12, 0);
-            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            acc[g >> 2][g & 3] = mfma_ab<SWAP>(a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -405,6 +413,7 @@ __device__ __forceinline__ void mainloop_a16(v16i (&acc)[TM][TN], const uint16_t
 
 // Accumulator element r of a 32x32 MFMA tile held by `lane`:
 //   row = (r/4)*8 + (lane/32)*4 + r%4,  col = lane%32.
+// With SWAP the roles trade: row = lane%32, col = acc_row(r, lane).
 __device__ __forceinline__ int acc_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 
 }  // namespace gemm

@@ -376,24 +376,95 @@ __device__ __forceinline__ void rq_tile_coords(int bid, int tiles_m, int tiles_n
     }
 }
 
-// The code of one fp16 value (low 16 bits of `bits`) with inverse scale inv, as
-// the low byte of a float's bits: clamp(h * inv) + 1.5 * 2^23 rounds half to
-// even onto the integer grid (|x| <= 128), like rint in requant_rows_kernel.
-__device__ __forceinline__ uint32_t rq_code_bits(uint32_t bits, float inv) {
+// Codes of the two fp16 values of `pair` with inverse scale inv, each as the low
+// byte of a float's bits: fl(h * inv) (one v_fma_mix rounding, the pass's
+// multiply; the sign of a zero product does not reach the code), clamped to
+// [-128, 127] when CLAMP, plus 1.5 * 2^23, which rounds half to even onto the
+// integer grid as rint does in requant_rows_kernel.  Without CLAMP the caller
+// guarantees |h * inv| < 127.5: every row max of the tile in [2^-14, 65504],
+// so h = fp16(v) <= amax (1 + 2^-11) + 2^-25 is finite.
+template <bool CLAMP>
+__device__ __forceinline__ void rq_codes2(uint32_t pair, float inv, uint32_t& lo, uint32_t& hi) {
 #pragma clang fp contract(off)
-    const float f = __half2float(__ushort_as_half((uint16_t)(bits & 0xffff))) * inv;
-    return __float_as_uint(fminf(fmaxf(f, -128.f), 127.f) + 12582912.0f);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 h = __builtin_bit_cast(h2, pair);
+    float a = __builtin_fmaf((float)h.x, inv, 0.0f);
+    float b = __builtin_fmaf((float)h.y, inv, 0.0f);
+    if constexpr (CLAMP) {
+        a = fminf(fmaxf(a, -128.f), 127.f);
+        b = fminf(fmaxf(b, -128.f), 127.f);
+    }
+    lo = __float_as_uint(a + 12582912.0f);
+    hi = __float_as_uint(b + 12582912.0f);
 }
 
-// 4 x 4 byte transpose across each aligned group of 4 lanes: lane m of the group
-// holds byte k = (row k, column m) and ends with byte k = (row m, column k).
-__device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t d, int lane) {
-    const uint32_t p2 = __builtin_amdgcn_mov_dpp(d, 0x4E, 0xF, 0xF, true);  // lane ^ 2
-    d = __builtin_amdgcn_perm(p2, d, (lane & 2) ? 0x03020706u : 0x05040100u);
-    const uint32_t p1 = __builtin_amdgcn_mov_dpp(d, 0xB1, 0xF, 0xF, true);  // lane ^ 1
-    return __builtin_amdgcn_perm(p1, d, (lane & 1) ? 0x03070105u : 0x06020400u);
+// Step 4 of the fused epilogue: the lane's codes go to LDS (the operand stages
+// are free by now) as a row-major 256 x 256-byte tile, one dword per 4 columns;
+// then each thread stores 16-byte pieces of whole rows, so a wave's store
+// covers 8 full 128-byte lines (the lanes of the accumulator layout span 32
+// rows, and direct stores from it wrote 32 partial lines per instruction).
+// h[i][j][k]: fp16 of the lane's columns 2k, 2k+1 (swapped accumulator layout).
+constexpr int kRqCodeStride = BN + 8;  // LDS bytes per staged row (8-byte aligned)
+static_assert(BM * kRqCodeStride <= LDS_BYTES, "the staged codes fit the operand stages");
+
+template <bool CLAMP>
+__device__ __forceinline__ void rq_store_codes(const uint32_t (&h)[TM][TN][8], const float* einv,
+                                               const RqParams& rq, int M, int N, int m0, int n0,
+                                               char* lds) {
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int rl = wm * WM + i * 32 + (lane & 31);
+        const float inv = einv[rl];
+        char* lrow = lds + rl * kRqCodeStride + wn * WN + (lane >> 5) * 4;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t c0, c1, c2, c3;
+                rq_codes2<CLAMP>(h[i][j][2 * q], inv, c0, c1);
+                rq_codes2<CLAMP>(h[i][j][2 * q + 1], inv, c2, c3);
+                *reinterpret_cast<uint32_t*>(lrow + j * 32 + q * 8) =
+                    __builtin_amdgcn_perm(c1, c0, 0x0c0c0400u) |
+                    __builtin_amdgcn_perm(c3, c2, 0x04000c0cu);
+            }
+        }
+    }
+    __syncthreads();
+    // 16 threads per row (N is a multiple of 16, so a piece is wholly in or out)
+    constexpr int kPieces = BM * BN / 16 / kThreads;
+    const bool vec = (reinterpret_cast<uintptr_t>(rq.q) & 15) == 0 && (rq.ldq & 15) == 0;
+    if (vec && m0 + BM <= M && n0 + BN <= N) {
+        int8_t* dst = rq.q + (size_t)(m0 + (t >> 4)) * rq.ldq + n0 + (t & 15) * 16;
+        const char* src = lds + (t >> 4) * kRqCodeStride + (t & 15) * 16;
+#pragma unroll
+        for (int k = 0; k < kPieces; ++k) {
+            // piece t + 256 k: row (t >> 4) + 16 k
+            const uint2 lo = *reinterpret_cast<const uint2*>(src + k * 16 * kRqCodeStride);
+            const uint2 hi = *reinterpret_cast<const uint2*>(src + k * 16 * kRqCodeStride + 8);
+            *reinterpret_cast<uint4*>(dst + (size_t)k * 16 * rq.ldq) =
+                make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+        return;
+    }
+    for (int k = 0; k < kPieces; ++k) {
+        const int c = t + k * kThreads;
+        const int row = c >> 4, col = (c & 15) * 16;
+        if (m0 + row < M && n0 + col < N) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(lds + row * kRqCodeStride + col);
+            uint32_t* d4 = reinterpret_cast<uint32_t*>(rq.q + (size_t)(m0 + row) * rq.ldq + n0 + col);
+            d4[0] = src[0], d4[1] = src[1], d4[2] = src[2], d4[3] = src[3];
+        }
+    }
 }
 
+// The fused epilogue on the swapped accumulator layout (mainloop<*, true>): lane
+// l holds row l % 32 of each 32-row block i and, for each column tile j, the
+// 16 columns (r/4)*8 + (l/32)*4 + r%4.  v and its row maxima as in
+// epilogue_interior; fp16 pairs of adjacent columns stay in registers.
 template <int EPI>
 __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const EpiParams& p,
                                             const RqParams& rq, int M, int N, int m0, int n0,
@@ -405,6 +476,7 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     const int lane = t & 63;
     const int wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5;
     int* rowmax = reinterpret_cast<int*>(lds);  // [2][BM]: per column half of the waves
     float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
     float* esb = esa + BM;
@@ -413,37 +485,34 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     esb[t] = pre_sb;
     ebias[t] = pre_b;
     __syncthreads();
-    // 1. values, their fp16 pairs (rows r, r+1 of the lane's column) and row maxima
+    // 1. values, fp16 pairs and the row max of |v| (columns past N excluded)
     uint32_t h[TM][TN][8];
-    float sbv[TN], biv[TN];
-    bool cok[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int cl = wn * WN + j * 32 + (lane & 31);
-        sbv[j] = esb[cl];
-        biv[j] = ebias[cl];
-        cok[j] = n0 + cl < N;
-    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        float sav[16], rmax[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 s4 =
-                *reinterpret_cast<const float4*>(esa + wm * WM + i * 32 + q * 8 + (lane >> 5) * 4);
-            sav[4 * q] = s4.x, sav[4 * q + 1] = s4.y, sav[4 * q + 2] = s4.z, sav[4 * q + 3] = s4.w;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) rmax[r] = 0.f;
+        const float sa = esa[wm * WM + i * 32 + (lane & 31)];
+        float rmax = 0.f;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
+            const int c0 = wn * WN + j * 32 + half * 4;  // + q * 8 + k
             float v[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) v[r] = static_cast<float>(acc[i][j][r]) * sav[r] * sbv[j];
+            for (int q = 0; q < 4; ++q) {
+                const float4 sb4 = *reinterpret_cast<const float4*>(esb + c0 + q * 8);
+                v[4 * q] = static_cast<float>(acc[i][j][4 * q]) * sa * sb4.x;
+                v[4 * q + 1] = static_cast<float>(acc[i][j][4 * q + 1]) * sa * sb4.y;
+                v[4 * q + 2] = static_cast<float>(acc[i][j][4 * q + 2]) * sa * sb4.z;
+                v[4 * q + 3] = static_cast<float>(acc[i][j][4 * q + 3]) * sa * sb4.w;
+            }
             if constexpr (EPI == EPI_GELU_F16) {
                 float e[16];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) v[r] = v[r] + biv[j];
+                for (int q = 0; q < 4; ++q) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(ebias + c0 + q * 8);
+                    v[4 * q] = v[4 * q] + b4.x;
+                    v[4 * q + 1] = v[4 * q + 1] + b4.y;
+                    v[4 * q + 2] = v[4 * q + 2] + b4.z;
+                    v[4 * q + 3] = v[4 * q + 3] + b4.w;
+                }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) e[r] = gelu_exponent(v[r]);
 #pragma unroll
@@ -453,15 +522,24 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
 #pragma unroll
                 for (int r = 0; r < 16; ++r) v[r] = v[r] * e[r];
             }
-            // columns past N do not count (their accumulators are zero, v need not be)
+            if (n0 + BN <= N) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) rmax[r] = fmaxf(rmax[r], cok[j] ? fabsf(v[r]) : 0.f);
+                for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, fabsf(v[r]));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (n0 + c0 + (r >> 2) * 8 + (r & 3) < N) rmax = fmaxf(rmax, fabsf(v[r]));
+            }
 #pragma unroll
             for (int r = 0; r < 16; r += 2)
                 h[i][j][r >> 1] =
                     __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){v[r], v[r + 1]}, h2));
         }
-        tile_rowmax(rmax, rowmax + wn * BM + wm * WM + i * 32, lane);
+        // lanes l and l ^ 32 hold the same row
+        const auto s = __builtin_amdgcn_permlane32_swap(__float_as_int(rmax), __float_as_int(rmax),
+                                                        false, false);
+        const int m = max((int)s[0], (int)s[1]);
+        if (half == 0) rowmax[wn * BM + wm * WM + i * 32 + lane] = m;
     }
     __syncthreads();
     // 2. publish the tile's row maxima, then its arrival
@@ -491,50 +569,21 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     __syncthreads();
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // the rows' inverse scales replace the row scales in LDS (last read before the barrier above)
+    // the rows' inverse scales replace the row scales in LDS (last read before the
+    // barrier after step 1); the clamp is needed only if a row max lies outside
+    // [2^-14, 65504]
+    bool wide;
     {
         const uint32_t bits = __hip_atomic_load(rq.amax + min(row_t, M - 1), __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
         const float amax = fmaxf(__uint_as_float(bits), 1e-8f);
         esa[t] = 127.f / amax;
         if (tn == 0 && row_t < M) rq.scales[row_t] = amax / 127.f;
+        wide = __syncthreads_or(!(amax >= 0x1p-14f && amax <= 65504.f)) != 0;
     }
-    __syncthreads();
-    // 4. codes: per (i, q) a lane holds rows base + 0..3 of its column for each j; packed into
-    // a dword and transposed across the 4 lanes of 4 consecutive columns, each lane stores
-    // row base + lane % 4, columns 4 * (lane % 32 / 4) .. + 3 of column tile j
-    const bool interior = m0 + BM <= M && n0 + BN <= N;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int rl = wm * WM + i * 32 + q * 8 + (lane >> 5) * 4;  // first of the 4 rows
-            const float4 inv4 = *reinterpret_cast<const float4*>(esa + rl);
-            uint32_t d[TN];
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const uint32_t w0 = h[i][j][2 * q], w1 = h[i][j][2 * q + 1];
-                const uint32_t c0 = rq_code_bits(w0, inv4.x), c1 = rq_code_bits(w0 >> 16, inv4.y);
-                const uint32_t c2 = rq_code_bits(w1, inv4.z), c3 = rq_code_bits(w1 >> 16, inv4.w);
-                const uint32_t col4 = __builtin_amdgcn_perm(c1, c0, 0x0c0c0400u) |
-                                      __builtin_amdgcn_perm(c3, c2, 0x04000c0cu);
-                d[j] = quad_transpose_bytes(col4, lane);
-            }
-            const int row = m0 + rl + (lane & 3);
-            const int cl = wn * WN + 4 * ((lane & 31) >> 2);
-            int8_t* dst = rq.q + (size_t)row * rq.ldq + n0 + cl;
-            if (interior) {
-#pragma unroll
-                for (int j = 0; j < TN; ++j) *reinterpret_cast<uint32_t*>(dst + j * 32) = d[j];
-            } else if (row < M) {
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-                        if (n0 + cl + j * 32 + b < N) dst[j * 32 + b] = (int8_t)(d[j] >> (8 * b));
-            }
-        }
-    }
+    // 4. codes (the row maxima in LDS were last read before the wait)
+    if (wide) rq_store_codes<true>(h, esa, rq, M, N, m0, n0, lds);
+    else rq_store_codes<false>(h, esa, rq, M, N, m0, n0, lds);
 }
 
 template <int EPI>
@@ -552,9 +601,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_rq_kernel(
     const float pre_b = p.bias != nullptr ? p.bias[min(n0 + t, N - 1)] : 0.f;
     v16i acc[TM][TN];
     if (m0 + BM <= M && n0 + BN <= N && K % BK == 0)
-        mainloop<false>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
+        mainloop<false, true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
     else
-        mainloop<true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
+        mainloop<true, true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
     epilogue_rq<EPI>(acc, p, rq, M, N, m0, n0, tm, tn, tiles_n, pre_sa, pre_sb, pre_b, lds);
 }
 
