@@ -384,79 +384,57 @@ __device__ __forceinline__ void rq_tile_coords(int bid, int tiles_m, int tiles_n
 // guarantees |h * inv| < 127.5: every row max of the tile in [2^-14, 65504],
 // so h = fp16(v) <= amax (1 + 2^-11) + 2^-25 is finite.
 template <bool CLAMP>
-__device__ __forceinline__ void rq_codes2(uint32_t pair, float inv, uint32_t& lo, uint32_t& hi) {
+__device__ __forceinline__ uint32_t rq_codes4(uint32_t p01, uint32_t p23, float inv) {
 #pragma clang fp contract(off)
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 h = __builtin_bit_cast(h2, pair);
-    float a = __builtin_fmaf((float)h.x, inv, 0.0f);
-    float b = __builtin_fmaf((float)h.y, inv, 0.0f);
-    if constexpr (CLAMP) {
-        a = fminf(fmaxf(a, -128.f), 127.f);
-        b = fminf(fmaxf(b, -128.f), 127.f);
+    const h2 a = __builtin_bit_cast(h2, p01), b = __builtin_bit_cast(h2, p23);
+    float f[4] = {__builtin_fmaf((float)a.x, inv, 0.0f), __builtin_fmaf((float)a.y, inv, 0.0f),
+                  __builtin_fmaf((float)b.x, inv, 0.0f), __builtin_fmaf((float)b.y, inv, 0.0f)};
+    uint32_t c[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (CLAMP) f[k] = fminf(fmaxf(f[k], -128.f), 127.f);
+        c[k] = __float_as_uint(f[k] + 12582912.0f);
     }
-    lo = __float_as_uint(a + 12582912.0f);
-    hi = __float_as_uint(b + 12582912.0f);
+    return __builtin_amdgcn_perm(c[1], c[0], 0x0c0c0400u) |
+           __builtin_amdgcn_perm(c[3], c[2], 0x04000c0cu);
 }
 
-// Step 4 of the fused epilogue: the lane's codes go to LDS (the operand stages
-// are free by now) as a row-major 256 x 256-byte tile, one dword per 4 columns;
-// then each thread stores 16-byte pieces of whole rows, so a wave's store
-// covers 8 full 128-byte lines (the lanes of the accumulator layout span 32
-// rows, and direct stores from it wrote 32 partial lines per instruction).
-// h[i][j][k]: fp16 of the lane's columns 2k, 2k+1 (swapped accumulator layout).
-constexpr int kRqCodeStride = BN + 8;  // LDS bytes per staged row (8-byte aligned)
-static_assert(BM * kRqCodeStride <= LDS_BYTES, "the staged codes fit the operand stages");
+// The fp16 tile waits in LDS (the operand stages are free after the main loop),
+// row-major with rows padded to kRqHStride bytes; the row maxima of the two
+// column halves of the waves follow it.
+constexpr int kRqHStride = 2 * BN + 8;
+constexpr int kRqRowmaxOff = BM * kRqHStride;
+static_assert(kRqRowmaxOff + 2 * BM * 4 <= LDS_BYTES, "fp16 tile and row maxima fit the stages");
 
+// Step 4 of the fused epilogue: each thread turns 16-column pieces of whole rows
+// of the staged fp16 tile into 16 codes and stores them as 16 bytes, so a
+// wave's store covers 8 full 128-byte lines.  einv: 127 / amax per tile row.
 template <bool CLAMP>
-__device__ __forceinline__ void rq_store_codes(const uint32_t (&h)[TM][TN][8], const float* einv,
-                                               const RqParams& rq, int M, int N, int m0, int n0,
-                                               char* lds) {
+__device__ __forceinline__ void rq_store_codes(const char* lds, const float* einv,
+                                               const RqParams& rq, int M, int N, int m0, int n0) {
     const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int rl = wm * WM + i * 32 + (lane & 31);
-        const float inv = einv[rl];
-        char* lrow = lds + rl * kRqCodeStride + wn * WN + (lane >> 5) * 4;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                uint32_t c0, c1, c2, c3;
-                rq_codes2<CLAMP>(h[i][j][2 * q], inv, c0, c1);
-                rq_codes2<CLAMP>(h[i][j][2 * q + 1], inv, c2, c3);
-                *reinterpret_cast<uint32_t*>(lrow + j * 32 + q * 8) =
-                    __builtin_amdgcn_perm(c1, c0, 0x0c0c0400u) |
-                    __builtin_amdgcn_perm(c3, c2, 0x04000c0cu);
-            }
-        }
-    }
-    __syncthreads();
-    // 16 threads per row (N is a multiple of 16, so a piece is wholly in or out)
-    constexpr int kPieces = BM * BN / 16 / kThreads;
+    constexpr int kPieces = BM * BN / 16 / kThreads;  // 16 per thread; 16 threads per row
+    const int g = t & 15;
     const bool vec = (reinterpret_cast<uintptr_t>(rq.q) & 15) == 0 && (rq.ldq & 15) == 0;
-    if (vec && m0 + BM <= M && n0 + BN <= N) {
-        int8_t* dst = rq.q + (size_t)(m0 + (t >> 4)) * rq.ldq + n0 + (t & 15) * 16;
-        const char* src = lds + (t >> 4) * kRqCodeStride + (t & 15) * 16;
-#pragma unroll
-        for (int k = 0; k < kPieces; ++k) {
-            // piece t + 256 k: row (t >> 4) + 16 k
-            const uint2 lo = *reinterpret_cast<const uint2*>(src + k * 16 * kRqCodeStride);
-            const uint2 hi = *reinterpret_cast<const uint2*>(src + k * 16 * kRqCodeStride + 8);
-            *reinterpret_cast<uint4*>(dst + (size_t)k * 16 * rq.ldq) =
-                make_uint4(lo.x, lo.y, hi.x, hi.y);
-        }
-        return;
-    }
+    const bool interior = vec && m0 + BM <= M && n0 + BN <= N;
+#pragma unroll 4
     for (int k = 0; k < kPieces; ++k) {
-        const int c = t + k * kThreads;
-        const int row = c >> 4, col = (c & 15) * 16;
-        if (m0 + row < M && n0 + col < N) {
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(lds + row * kRqCodeStride + col);
-            uint32_t* d4 = reinterpret_cast<uint32_t*>(rq.q + (size_t)(m0 + row) * rq.ldq + n0 + col);
-            d4[0] = src[0], d4[1] = src[1], d4[2] = src[2], d4[3] = src[3];
+        const int row = (t >> 4) + 16 * k;
+        const float inv = einv[row];
+        const uint2* src = reinterpret_cast<const uint2*>(lds + row * kRqHStride + g * 32);
+        const uint2 h0 = src[0], h1 = src[1], h2v = src[2], h3 = src[3];
+        const uint4 c = make_uint4(rq_codes4<CLAMP>(h0.x, h0.y, inv),
+                                   rq_codes4<CLAMP>(h1.x, h1.y, inv),
+                                   rq_codes4<CLAMP>(h2v.x, h2v.y, inv),
+                                   rq_codes4<CLAMP>(h3.x, h3.y, inv));
+        int8_t* dst = rq.q + (size_t)(m0 + row) * rq.ldq + n0 + g * 16;
+        if (interior) {
+            *reinterpret_cast<uint4*>(dst) = c;
+        } else if (m0 + row < M && n0 + g * 16 < N) {
+            // N is a multiple of 16: a piece is wholly in or out
+            uint32_t* d4 = reinterpret_cast<uint32_t*>(dst);
+            d4[0] = c.x, d4[1] = c.y, d4[2] = c.z, d4[3] = c.w;
         }
     }
 }
@@ -464,12 +442,13 @@ __device__ __forceinline__ void rq_store_codes(const uint32_t (&h)[TM][TN][8], c
 // The fused epilogue on the swapped accumulator layout (mainloop<*, true>): lane
 // l holds row l % 32 of each 32-row block i and, for each column tile j, the
 // 16 columns (r/4)*8 + (l/32)*4 + r%4.  v and its row maxima as in
-// epilogue_interior; fp16 pairs of adjacent columns stay in registers.
+// epilogue_interior; fp16(v) goes to LDS right away, so no value is held in
+// registers across the wait.
 template <int EPI>
-__device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const EpiParams& p,
-                                            const RqParams& rq, int M, int N, int m0, int n0,
-                                            int tm, int tn, int tiles_n, float pre_sa,
-                                            float pre_sb, float pre_b, char* lds) {
+__device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const RqParams& rq,
+                                            int M, int N, int m0, int n0, int tm, int tn,
+                                            int tiles_n, float pre_sa, float pre_sb,
+                                            float pre_b, char* lds) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     typedef float f2 __attribute__((ext_vector_type(2)));
     const int t = threadIdx.x;
@@ -477,7 +456,7 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     const int wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5;
-    int* rowmax = reinterpret_cast<int*>(lds);  // [2][BM]: per column half of the waves
+    int* rowmax = reinterpret_cast<int*>(lds + kRqRowmaxOff);  // [2][BM]
     float* esa = reinterpret_cast<float*>(lds + LDS_BYTES);
     float* esb = esa + BM;
     float* ebias = esb + BM;
@@ -485,11 +464,12 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     esb[t] = pre_sb;
     ebias[t] = pre_b;
     __syncthreads();
-    // 1. values, fp16 pairs and the row max of |v| (columns past N excluded)
-    uint32_t h[TM][TN][8];
+    // 1. values, the row max of |v| (columns past N excluded), fp16 pairs to LDS
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        const float sa = esa[wm * WM + i * 32 + (lane & 31)];
+        const int rl = wm * WM + i * 32 + (lane & 31);
+        const float sa = esa[rl];
+        char* hrow = lds + rl * kRqHStride;
         float rmax = 0.f;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -531,15 +511,19 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
                     if (n0 + c0 + (r >> 2) * 8 + (r & 3) < N) rmax = fmaxf(rmax, fabsf(v[r]));
             }
 #pragma unroll
-            for (int r = 0; r < 16; r += 2)
-                h[i][j][r >> 1] =
-                    __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){v[r], v[r + 1]}, h2));
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t p01 = __builtin_bit_cast(
+                    uint32_t, __builtin_convertvector((f2){v[4 * q], v[4 * q + 1]}, h2));
+                const uint32_t p23 = __builtin_bit_cast(
+                    uint32_t, __builtin_convertvector((f2){v[4 * q + 2], v[4 * q + 3]}, h2));
+                *reinterpret_cast<uint2*>(hrow + (c0 + q * 8) * 2) = make_uint2(p01, p23);
+            }
         }
         // lanes l and l ^ 32 hold the same row
         const auto s = __builtin_amdgcn_permlane32_swap(__float_as_int(rmax), __float_as_int(rmax),
                                                         false, false);
         const int m = max((int)s[0], (int)s[1]);
-        if (half == 0) rowmax[wn * BM + wm * WM + i * 32 + lane] = m;
+        if (half == 0) rowmax[wn * BM + rl] = m;
     }
     __syncthreads();
     // 2. publish the tile's row maxima, then its arrival
@@ -553,11 +537,13 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
     __syncthreads();
     if (t == 0) {
-        __hip_atomic_fetch_add(rq.arrived + tm, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // 3. wait for the stripe's other tiles
+        // 3. wait for the stripe's other tiles (the last to arrive need not)
+        const uint32_t before = __hip_atomic_fetch_add(rq.arrived + tm, 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        while (__hip_atomic_load(rq.arrived + tm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-               (uint32_t)tiles_n) {
+        while (before + 1 < (uint32_t)tiles_n &&
+               __hip_atomic_load(rq.arrived + tm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                   (uint32_t)tiles_n) {
             __builtin_amdgcn_s_sleep(2);
             if (__builtin_amdgcn_s_memrealtime() - t0 > kRqWaitTicks) {
                 __hip_atomic_fetch_add(&g_rq_timeouts, 1u, __ATOMIC_RELAXED,
@@ -569,9 +555,8 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
     __syncthreads();
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // the rows' inverse scales replace the row scales in LDS (last read before the
-    // barrier after step 1); the clamp is needed only if a row max lies outside
-    // [2^-14, 65504]
+    // the rows' inverse scales replace the row scales in LDS (last read in step 1);
+    // the clamp is needed only if a row max lies outside [2^-14, 65504]
     bool wide;
     {
         const uint32_t bits = __hip_atomic_load(rq.amax + min(row_t, M - 1), __ATOMIC_RELAXED,
@@ -581,9 +566,9 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const Epi
         if (tn == 0 && row_t < M) rq.scales[row_t] = amax / 127.f;
         wide = __syncthreads_or(!(amax >= 0x1p-14f && amax <= 65504.f)) != 0;
     }
-    // 4. codes (the row maxima in LDS were last read before the wait)
-    if (wide) rq_store_codes<true>(h, esa, rq, M, N, m0, n0, lds);
-    else rq_store_codes<false>(h, esa, rq, M, N, m0, n0, lds);
+    // 4. codes
+    if (wide) rq_store_codes<true>(lds, esa, rq, M, N, m0, n0);
+    else rq_store_codes<false>(lds, esa, rq, M, N, m0, n0);
 }
 
 template <int EPI>
@@ -604,7 +589,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_rq_kernel(
         mainloop<false, true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
     else
         mainloop<true, true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
-    epilogue_rq<EPI>(acc, p, rq, M, N, m0, n0, tm, tn, tiles_n, pre_sa, pre_sb, pre_b, lds);
+    epilogue_rq<EPI>(acc, rq, M, N, m0, n0, tm, tn, tiles_n, pre_sa, pre_sb, pre_b, lds);
 }
 
 // Zeroes n dwords (the fused requant's amax and arrival counters) before the GEMMs.
