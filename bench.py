@@ -812,11 +812,25 @@ def bench_gemm(args):
     if not torch.equal(C[:64].cpu().double(), ref):
         raise SystemExit("gemm_i8_i32 does not match the exact int32 product")
     ms_lib = time_steps(lambda: torch._int_mm(A, Bt.t()), args.steps, args.warmup, stream)
+    # the MLP's own operands: config 4's per-token x and per-channel W1 codes (Gaussian data)
+    import workloads
+
+    c = workloads.mlp_case(M, K, N, seed=args.seed, device=dev)
+    Am = c["x"].reshape(M, K).contiguous()
+    Bm = c["W1"].t().contiguous()  # [N][K]
+    del c
+    ms_mlp = time_steps(lambda: capi.gemm_i8_i32(Am, Bm, out=C), args.steps, args.warmup, stream)
+    ref = Am[:64].double().cpu() @ Bm.double().cpu().t()
+    if not torch.equal(C[:64].cpu().double(), ref):
+        raise SystemExit("gemm_i8_i32 does not match the exact int32 product (MLP operands)")
+    ms_lib_mlp = time_steps(lambda: torch._int_mm(Am, Bm.t()), args.steps, args.warmup, stream)
+    del Am, Bm
     A.zero_()
     Bt.zero_()
     ms_zero = time_steps(lambda: capi.gemm_i8_i32(A, Bt, out=C), args.steps, args.warmup, stream)
     tops = ops / (ms_rand * 1e-3) / 1e12
-    for name, ms in (("random", ms_rand), ("zero", ms_zero), ("hipblaslt random", ms_lib)):
+    for name, ms in (("random", ms_rand), ("zero", ms_zero), ("hipblaslt random", ms_lib),
+                     ("mlp operands", ms_mlp), ("hipblaslt mlp operands", ms_lib_mlp)):
         log(f"[bench] gemm {name}: {ms * 1e3:.1f} us  {ops / (ms * 1e-3) / 1e12:.1f} TOPS")
     L = ctypes.CDLL(os.path.join(PKG_DIR, "libint8k_calib.so"))
     return {
@@ -827,7 +841,9 @@ def bench_gemm(args):
         "data": "synthetic uniform random int8 (and all-zero for the comparison)",
         "config": {"workload": "int8 GEMM M=4096 N=16384 K=4096",
                    "zero_operands_TOPS": round(ops / (ms_zero * 1e-3) / 1e12, 1),
-                   "hipblaslt_int_mm_random_TOPS": round(ops / (ms_lib * 1e-3) / 1e12, 1)},
+                   "hipblaslt_int_mm_random_TOPS": round(ops / (ms_lib * 1e-3) / 1e12, 1),
+                   "mlp_operands_us": round(ms_mlp * 1e3, 2),
+                   "hipblaslt_int_mm_mlp_operands_us": round(ms_lib_mlp * 1e3, 2)},
         "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                      "traffic": None, "kernel": "gemm_i8_kernel<0>"},

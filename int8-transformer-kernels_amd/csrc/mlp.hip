@@ -13,11 +13,16 @@
 //   epi2    o = (f32(acc2) * sh[t]) * sW2[n];  out16 = fp16(o);  rowmax / tensor max of |o|
 //   quant   out = rn(clamp(f32(out16) * 127/amax)),  out_scale = amax/127 (per token or tensor)
 //
-// Kernels: gemm_i8_kernel<EPI> (the MFMA core of gemm_i8.h with a fused
-// epilogue: scales, bias, GELU, fp16 store and per-(tile, row) absmax partials
-// — no atomics, no zero-fill), requant_rows_kernel (reduces the partials,
-// requantizes a row), tensor_absmax_kernel and transpose_i8_kernel (weight
-// packing to the K-contiguous [N][K] layout the MFMA operands want).
+// Kernels: gemm_i8_rq_kernel<EPI> (the MFMA core of gemm_i8.h whose epilogue
+// finishes the per-token requantization itself: the tiles of a 256-row stripe
+// exchange their row maxima through device-scope atomics and emit int8 codes,
+// so neither the fp16 hidden nor the fp16 output reaches memory — the default
+// wherever a GEMM runs 256 x 256 tiles), gemm_i8_kernel<EPI> (the same core with
+// an fp16 epilogue: scales, bias, GELU, fp16 store and per-(tile, row) absmax
+// partials), requant_rows_kernel (reduces the partials, requantizes a row; the
+// path of the other tilings and of INT8K_MLP_SEPARATE_REQUANT),
+// tensor_absmax_kernel and transpose_i8_kernel (weight packing to the
+// K-contiguous [N][K] layout the MFMA operands want).
 // gemm_i8_a16_kernel is GEMM2 reading the fp16 hidden and quantizing it per
 // row on load (no requant pass, no int8 hidden in memory); same bytes, slower
 // on MI355X, so it runs only when INT8K_MLP_GEMM2_FP16_HIDDEN=1.
@@ -1560,7 +1565,8 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
         W1t = w.w1t;
         W2t = w.w2t;
     }
-    // GEMM1 + scale/bias/GELU epilogue -> fp16 hidden + row absmax partials
+    // GEMM1 + scale/bias/GELU epilogue -> int8 hidden + row scales (fused requant), or
+    // fp16 hidden + row absmax partials for the separate pass
     EpiParams p1{};
     p1.c16 = w.h16;
     p1.ldc = d_ff;
@@ -1583,7 +1589,8 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     else
         st = launch_gemm<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     if (st != INT8K_OK) return st;
-    // GEMM2 + dequant epilogue -> fp16 output + absmax partials
+    // GEMM2 + dequant epilogue -> int8 output + scales (fused requant), or fp16 output +
+    // absmax partials for the separate pass
     const int tn1 = epi_tiles(T, d_ff, d_model);
     EpiParams p2{};
     p2.c16 = w.o16;
