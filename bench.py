@@ -274,7 +274,8 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
         if rc != 0:
             capi.check("int8k_decode_attention_forward", rc)
 
-    ms, windows = time_windows(step, args.steps, args.warmup, stream)
+    # every cache copy is touched before the first timed window
+    ms, windows = time_windows(step, args.steps, max(args.warmup, 2 * n_copies), stream)
     K, V, sK, sV = kv
     out.zero_()
     capi.decode_attention(Q, K, V, sQ, sK, sV, nsplit=args.nsplit, out=out, workspace=ws)
@@ -508,6 +509,97 @@ def bench_decode_paged(args):
                                 else "decode_paged_kernel + decode_combine_kernel (one step)")},
         "cpu_baseline": None,
     }
+
+
+def measure_paged(B, H, D, S, pages, args, dev, stream):
+    """Paged decode at one shape for each page size in `pages`: the contiguous case's data
+    (same seed) cut into pages stored in a seeded random physical order, one block-table row
+    per sequence, every length = S.  Timed as measure_decode (median of 5 windows; cases
+    under 512 MB cycle through cache copies), with every (b,h) row checked against the C
+    oracle.  The contiguous kernel's line for the same shape and seed sits beside it."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import int8k_capi as capi
+    import workloads
+    from oracle import oracle_c
+
+    BH = B * H
+    case = workloads.decode_case(B, H, D, S, seed=args.seed, outlier_frac=0.01, device=dev)
+    host = [case[k].cpu().numpy() for k in ("Qi", "Ki", "Vi", "sQ", "sK", "sV")]
+    ref = oracle_c.decode_attention(host[0].reshape(BH, D), host[1].reshape(BH, S, D),
+                                    host[2].reshape(BH, S, D), host[3].reshape(BH),
+                                    host[4].reshape(BH, S), host[5].reshape(BH, S))
+    del host
+    lib = capi.load()
+    Pt = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(stream.cuda_stream)
+    kv_bytes = 2 * BH * S * D
+
+    def check(out, what):
+        got = out.float().reshape(BH, D).cpu().numpy()
+        err = float(np.abs(got - ref).max())
+        cos = float((got * ref).sum() / max(np.linalg.norm(got) * np.linalg.norm(ref), 1e-30))
+        if not (err <= 2e-2 and cos >= 0.9999):
+            raise SystemExit(f"{what} does not match the oracle (max_abs={err}, cos={cos})")
+        return {"rows_checked": BH, "max_abs": err, "cos": round(cos, 7)}
+
+    rows = []
+    for P in pages:
+        npp = -(-S // P)
+        NP = B * npp
+        perm = torch.randperm(NP, generator=torch.Generator().manual_seed(args.seed + P)).to(dev)
+
+        def to_pages(x):  # [B, H, S, ...] -> [NP, H, P, ...]; page (b, i) at perm[b*npp + i]
+            tail = tuple(x.shape[3:])
+            pad = torch.zeros((B, H, npp * P) + tail, dtype=x.dtype, device=dev)
+            pad[:, :, :S] = x
+            pg = pad.reshape((B, H, npp, P) + tail).movedim(2, 1).reshape((NP, H, P) + tail)
+            o = torch.empty_like(pg)
+            o[perm] = pg
+            return o
+
+        cache = (to_pages(case["Ki"]), to_pages(case["Vi"]), to_pages(case["sK"]),
+                 to_pages(case["sV"]))
+        total = kv_bytes + 2 * BH * S * 4
+        n_copies = 1 if total >= (512 << 20) else max(3, -(-(768 << 20) // total))
+        copies = [cache] + [tuple(t.clone() for t in cache) for _ in range(n_copies - 1)]
+        tables = perm.to(torch.int32).reshape(B, npp).contiguous()
+        lens = torch.full((B,), S, dtype=torch.int32, device=dev)
+        out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
+        ws = torch.empty(max(capi.decode_paged_workspace_bytes(B, H, S, D, args.nsplit), 1),
+                         dtype=torch.uint8, device=dev)
+        calls = [(Pt(case["Qi"]), Pt(Kp), Pt(Vp), Pt(out), Pt(case["sQ"]), Pt(sKp), Pt(sVp),
+                  Pt(tables), Pt(lens), B, H, D, NP, P, npp, S, args.nsplit, Pt(ws), ws.numel(),
+                  st) for (Kp, Vp, sKp, sVp) in copies]
+        it = [0]
+
+        def step():
+            a = calls[it[0] % n_copies]
+            it[0] += 1
+            rc = lib.int8k_decode_attention_forward_paged(*a)
+            if rc != 0:
+                capi.check("int8k_decode_attention_forward_paged", rc)
+
+        ms, windows = time_windows(step, args.steps, max(args.warmup, 2 * n_copies), stream)
+        out.zero_()
+        it[0] = 0
+        step()
+        torch.cuda.synchronize()
+        parity = check(out, f"paged decode B{B} H{H} D{D} S{S} page {P}")
+        tbs = kv_bytes / (ms * 1e-3) / 1e12
+        rows.append({"B": B, "H": H, "D": D, "ctx": S, "page": P,
+                     "nsplit": capi.decode_paged_num_splits(B, H, S, D, args.nsplit),
+                     "us": round(ms * 1e3, 2), "TBps": round(tbs, 4),
+                     "pct_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS * 100, 2),
+                     "windows_ms": windows, "cache_copies": n_copies, "parity": parity})
+        log(f"[bench] paged decode B{B} H{H} D{D} ctx{S} page {P}: {ms * 1e3:.1f} us "
+            f"{tbs:.3f} TB/s, all {BH} rows vs oracle: max_abs {parity['max_abs']:.1e}")
+        del copies, cache, calls, ws
+        torch.cuda.empty_cache()
+    return rows
 
 
 INT8_PEAK_TOPS = 5000.0
@@ -770,6 +862,10 @@ def bench_all(args):
         log(f"[bench] cfg1 torch-CPU: {cfg1['cpu_baseline']['us']} us "
             f"(1 thread {cfg1['cpu_baseline']['one_thread_us']} us)")
     torch.cuda.empty_cache()
+    paged = (measure_paged(args.batch, args.heads, args.head_dim, args.ctx, (16, 256), args, dev,
+                           stream)
+             + measure_paged(8, 32, 64, 32768, (16, 256), args, dev, stream))
+    torch.cuda.empty_cache()
     cfg4 = measure_mlp(args, dev, stream, None if args.no_cpu_baseline else 5.0)
     torch.cuda.empty_cache()
     cfg5 = measure_prefill(args, dev, stream, None if args.no_cpu_baseline else 5.0,
@@ -780,6 +876,7 @@ def bench_all(args):
         "cfg1_decode_b1h12d64_s1024": cfg1,
         "cfg3_decode_b8h32d64_s32768": sweep[-1],
         "cfg3_ctx_sweep_b8h32d64": sweep[:-1],
+        "paged_decode": paged,
         "cfg4_mlp_t4096_d4096_f16384": cfg4,
         "cfg5_prefill_causal_b4h32s4096d128": cfg5,
         "block_d1024_h16_dff4096": {"metric": blk["metric"], "value": blk["value"],
