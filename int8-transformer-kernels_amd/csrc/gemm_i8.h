@@ -147,18 +147,71 @@ __device__ __forceinline__ void mfma_slice(v16i (&acc)[TM][TN], const v4i (&a)[T
             acc[i][j] = mfma_ab<SWAP>(a[i], b[j], acc[i][j]);
 }
 
+// ------------------------------------------------------------ B stored [K][N]
+// The MLP's weights as the caller holds them (W1 [d_model][d_ff], W2 [d_ff][d_model])
+// are N-contiguous.  With BKN the main loop stages the B tile as it arrives, BK
+// rows of k with the tile's BN bytes of n each (rows padded to KN_STRIDE), and
+// forms each K-contiguous MFMA fragment with two transposing LDS reads
+// (ds_read_b64_tr_b8), so no weight transpose runs.  Measured on the box: in each
+// group of 16 lanes, the instruction gives lane 8h + b byte b of the 8-byte rows
+// that lanes h, h+2, ..., h+14 address.  Lane s of group g therefore addresses
+// row 16 (g/2) + s/2 at columns 16 (g%2) + 8 (s%2): lane l then holds
+// k = 16 (l/32) + 0..7 of column l % 32, the B fragment's layout, and a second
+// read 8 rows further gives k + 8..15.
+constexpr int KN_STRIDE = BN + 32;  // 288 B: the 16 rows of one read start 32 B apart in the banks
+static_assert(BK * KN_STRIDE == B_STAGE, "the [K][N] B tile takes the stage bytes of [N][K]");
+
+// Chunk i of this thread of a [K][N] B tile: k row c / 16, n bytes (c % 16) * 16
+// (16 threads per 256-byte row).  N % 16 == 0; chunks past K or N read a clamped
+// address and are zeroed when stored (EDGE).
+__device__ __forceinline__ int4 load_chunk_kn(const int8_t* __restrict__ W, int K, int N, int ldw,
+                                              int k0, int n0, int i) {
+    const int c = threadIdx.x + i * kThreads;
+    const int kr = c >> 4, nc = (c & 15) * 16;
+    return *reinterpret_cast<const int4*>(W + (size_t)min(k0 + kr, K - 1) * ldw +
+                                          min(n0 + nc, N - 16));
+}
+
+template <bool EDGE>
+__device__ __forceinline__ void store_chunk_kn(int4 v, char* lds_b, int K, int N, int k0, int n0,
+                                               int i) {
+    const int c = threadIdx.x + i * kThreads;
+    const int kr = c >> 4, nc = (c & 15) * 16;
+    if constexpr (EDGE) {
+        if (!(k0 + kr < K && n0 + nc < N)) v = make_int4(0, 0, 0, 0);
+    }
+    *reinterpret_cast<int4*>(lds_b + kr * KN_STRIDE + nc) = v;
+}
+
+// This lane's address inside a [K][N] B stage for fragment reads (see above).
+__device__ __forceinline__ int kn_frag_offset(int lane, int wn) {
+    const int g = lane >> 4, s = lane & 15;
+    return (16 * (g >> 1) + (s >> 1)) * KN_STRIDE + wn * WN + 16 * (g & 1) + 8 * (s & 1);
+}
+
+// B fragment of column tile j, k-slice `slice`, from a [K][N] stage.
+__device__ __forceinline__ v4i read_frag_kn(const char* stage_b, int off, int j, int slice) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) v2i lds_v2i;
+    const char* p = stage_b + off + slice * 32 * KN_STRIDE + j * 32;
+    const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(p));
+    const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(p + 8 * KN_STRIDE));
+    return v4i{lo.x, lo.y, hi.x, hi.y};
+}
+
 // Instruction classes for __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100,
               kSchedDsWrite = 0x200;
 
-// 8 LDS reads interleaved with the first 8 of 16 MFMAs.
+// NR LDS reads interleaved with the first NR of 16 MFMAs.
+template <int NR = 8>
 __device__ __forceinline__ void sched_reads_mfma() {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NR; ++i) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 16 - NR, 0);
 }
 
 // The MFMA main loop: acc[i][j] (32x32 tiles) of this wave's 128x128 sub-tile.
@@ -176,7 +229,8 @@ __device__ __forceinline__ void sched_reads_mfma() {
 // Writing buffer (kt+1)&1 during step kt is safe: its last reads (step kt-1)
 // completed before step kt-1's barrier.  Past the end of K the loads clamp to
 // valid addresses and the writes land in the buffer nobody reads again.
-template <bool EDGE, bool SWAP = false>
+// BKN: Bt is B stored [K][N] (row stride ldb), staged and read as above.
+template <bool EDGE, bool SWAP = false, bool BKN = false>
 __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __restrict__ A,
                                          const int8_t* __restrict__ Bt, int M, int N, int K,
                                          int lda, int ldb, int m0, int n0, char* lds) {
@@ -195,25 +249,56 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
     const int nk = (K + BK - 1) / BK;
     // fragment read offsets inside a stage: row (l%32), 16-byte half (l/32)
     const int a_off = (wm * WM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
-    const int b_off = A_STAGE + (wn * WN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    const int b_off = BKN ? kn_frag_offset(lane, wn)
+                          : A_STAGE + (wn * WN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
+    auto load_b = [&](int k0, int i) {
+        return BKN ? load_chunk_kn(Bt, K, N, ldb, k0, n0, i) : load_chunk(Bt, N, K, ldb, n0, k0, i);
+    };
+    auto store_b = [&](int4 v, char* stage, int k0, int i) {
+        if constexpr (BKN) store_chunk_kn<EDGE>(v, stage + A_STAGE, K, N, k0, n0, i);
+        else store_chunk<EDGE>(v, stage + A_STAGE, N, K, n0, k0, i);
+    };
+    auto read_b = [&](const char* stage, int j, int slice) {
+        return BKN ? read_frag_kn(stage + A_STAGE, b_off, j, slice)
+                   : read_frag(stage, b_off, j, slice);
+    };
+    auto read_ab = [&](v4i (&a)[TM], v4i (&b)[TN], const char* stage, int slice) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = read_frag(stage, a_off, i, slice);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[j] = read_b(stage, j, slice);
+    };
+    constexpr int kReads = BKN ? TM + 2 * TN : TM + TN;  // LDS read instructions per slice
     Frag f;
-    load_stage(f, A, Bt, M, N, K, lda, ldb, m0, n0, 0);
-    store_stage<EDGE>(f, lds, M, N, K, m0, n0, 0);
-    load_stage(f, A, Bt, M, N, K, lda, ldb, m0, n0, BK);
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        f.a[i] = load_chunk(A, M, K, lda, m0, 0, i);
+        f.b[i] = load_b(0, i);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        store_chunk<EDGE>(f.a[i], lds, M, K, m0, 0, i);
+        store_b(f.b[i], lds, 0, i);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        f.a[i] = load_chunk(A, M, K, lda, m0, BK, i);
+        f.b[i] = load_b(BK, i);
+    }
     __syncthreads();
     v4i a[2][TM], b[2][TN];
-    read_slice(a[0], b[0], lds, a_off, b_off, 0);
+    read_ab(a[0], b[0], lds, 0);
     for (int kt = 0; kt < nk; ++kt) {
         const char* cur = lds + (kt & 1) * STAGE_BYTES;
         char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
         __builtin_amdgcn_sched_barrier(0);
-        read_slice(a[1], b[1], cur, a_off, b_off, 1);
+        read_ab(a[1], b[1], cur, 1);
         mfma_slice<SWAP>(acc, a[0], b[0]);
-        sched_reads_mfma();
+        sched_reads_mfma<kReads>();
         __builtin_amdgcn_sched_barrier(0);
-        read_slice(a[0], b[0], cur, a_off, b_off, 2);
+        read_ab(a[0], b[0], cur, 2);
         mfma_slice<SWAP>(acc, a[1], b[1]);
-        sched_reads_mfma();
+        sched_reads_mfma<kReads>();
         __builtin_amdgcn_sched_barrier(0);
         // slice 2, one group per MFMA: a fragment read of slice 3, a chunk
         // written to the next stage and its replacement load, then the MFMA
@@ -221,13 +306,13 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
         for (int g = 0; g < 16; ++g) {
             const int i = g >> 2, j = g & 3;
             if (g < 4) a[1][g] = read_frag(cur, a_off, g, 3);
-            else if (g < 8) b[1][g - 4] = read_frag(cur, b_off, g - 4, 3);
+            else if (g < 8) b[1][g - 4] = read_b(cur, g - 4, 3);
             if (g < 8) {
                 store_chunk<EDGE>(f.a[g], nxt, M, K, m0, (kt + 1) * BK, g);
                 f.a[g] = load_chunk(A, M, K, lda, m0, (kt + 2) * BK, g);
             } else {
-                store_chunk<EDGE>(f.b[g - 8], nxt + A_STAGE, N, K, n0, (kt + 1) * BK, g - 8);
-                f.b[g - 8] = load_chunk(Bt, N, K, ldb, n0, (kt + 2) * BK, g - 8);
+                store_b(f.b[g - 8], nxt, (kt + 1) * BK, g - 8);
+                f.b[g - 8] = load_b((kt + 2) * BK, g - 8);
             }
             acc[i][j] = mfma_ab<SWAP>(a[0][i], b[0][j], acc[i][j]);
             __builtin_amdgcn_sched_barrier(0);
@@ -243,7 +328,7 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
 #pragma unroll
         for (int g = 8; g < 16; ++g) {
             if (g < 12) a[0][g - 8] = read_frag(nxt, a_off, g - 8, 0);
-            else b[0][g - 12] = read_frag(nxt, b_off, g - 12, 0);
+            else b[0][g - 12] = read_b(nxt, g - 12, 0);
             acc[g >> 2][g & 3] = mfma_ab<SWAP>(a[1][g >> 2], b[1][g & 3], acc[g >> 2][g & 3]);
             __builtin_amdgcn_sched_barrier(0);
         }

@@ -274,7 +274,8 @@ __device__ __forceinline__ void epilogue_tile(const v16i (&acc)[TM_][TN_], const
             __int_as_float(max(rowmax[threadIdx.x], rowmax[BM_ + threadIdx.x]));
 }
 
-template <int EPI>
+// BKN: Bt is B stored [K][N] (ldb = its row stride), read without a transpose.
+template <int EPI, bool BKN = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int M, int N, int K, int lda,
     int ldb, int tiles_m, int tiles_n, EpiParams p) {
@@ -294,9 +295,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     v16i acc[TM][TN];
     // interior tiles take the unmasked operand path
     if (m0 + BM <= M && n0 + BN <= N && K % BK == 0)
-        mainloop<false>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
+        mainloop<false, false, BKN>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
     else
-        mainloop<true>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
+        mainloop<true, false, BKN>(acc, A, Bt, M, N, K, lda, ldb, m0, n0, lds);
 
     if constexpr (EPI == EPI_I32) {
         const int lane = threadIdx.x & 63;
@@ -576,7 +577,8 @@ __device__ __forceinline__ void epilogue_rq(const v16i (&acc)[TM][TN], const RqP
     else rq_store_codes<false>(lds, esa, rq, M, N, m0, n0);
 }
 
-template <int EPI>
+// BKN: Bt is B stored [K][N] (row stride N), read without a transpose.
+template <int EPI, bool BKN = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_i8_rq_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ Bt, int M, int N, int K,
     int tiles_m, int tiles_n, EpiParams p, RqParams rq) {
@@ -590,10 +592,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_rq_kernel(
     const float pre_sb = p.sb[(size_t)min(n0 + t, N - 1) * p.sb_stride];
     const float pre_b = p.bias != nullptr ? p.bias[min(n0 + t, N - 1)] : 0.f;
     v16i acc[TM][TN];
+    const int ldb = BKN ? N : K;
     if (m0 + BM <= M && n0 + BN <= N && K % BK == 0)
-        mainloop<false, true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
+        mainloop<false, true, BKN>(acc, A, Bt, M, N, K, K, ldb, m0, n0, lds);
     else
-        mainloop<true, true>(acc, A, Bt, M, N, K, K, K, m0, n0, lds);
+        mainloop<true, true, BKN>(acc, A, Bt, M, N, K, K, ldb, m0, n0, lds);
     epilogue_rq<EPI>(acc, rq, M, N, m0, n0, tm, tn, tiles_n, pre_sa, pre_sb, pre_b, lds);
 }
 
@@ -1278,13 +1281,13 @@ __global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restr
     }
 }
 
-template <int EPI>
+template <int EPI, bool BKN = false>
 int launch_gemm(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
                 hipStream_t stream) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    gemm_i8_kernel<EPI><<<tiles_m * tiles_n, kThreads, EPI == EPI_I32 ? LDS_BYTES : kEpiLdsBytes,
-                          stream>>>(
-        A, Bt, M, N, K, K, K, tiles_m, tiles_n, p);
+    gemm_i8_kernel<EPI, BKN>
+        <<<tiles_m * tiles_n, kThreads, EPI == EPI_I32 ? LDS_BYTES : kEpiLdsBytes, stream>>>(
+            A, Bt, M, N, K, K, BKN ? N : K, tiles_m, tiles_n, p);
     return check_launch("gemm_i8_kernel");
 }
 
@@ -1327,7 +1330,7 @@ RqParams rq_layout(int tiles_m, int tiles_n) {
 
 // A GEMM with the per-token requantization in its epilogue: codes q [M][N] and
 // row scales; amax [M] and arrived [tiles_m] must be zero.
-template <int EPI>
+template <int EPI, bool BKN = false>
 int launch_gemm_rq(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
                    int8_t* q, float* scales, uint32_t* amax, uint32_t* arrived,
                    hipStream_t stream) {
@@ -1338,7 +1341,7 @@ int launch_gemm_rq(const int8_t* A, const int8_t* Bt, int M, int N, int K, const
     rq.scales = scales;
     rq.amax = amax;
     rq.arrived = arrived;
-    gemm_i8_rq_kernel<EPI><<<tiles_m * tiles_n, kThreads, kEpiLdsBytes, stream>>>(
+    gemm_i8_rq_kernel<EPI, BKN><<<tiles_m * tiles_n, kThreads, kEpiLdsBytes, stream>>>(
         A, Bt, M, N, K, tiles_m, tiles_n, p, rq);
     return check_launch("gemm_i8_rq_kernel");
 }
@@ -1388,6 +1391,31 @@ RqPlan rq_plan(int T, int dm, int dff, int flags) {
     return pl;
 }
 
+// Whether a GEMM runs on the 256 x 256 tiled kernels (gemm_i8_kernel, gemm_i8_rq_kernel).
+inline bool tiled_256(int M, int N, int K) {
+    return !use_skinny(M, N, K) && !splitk_plan(M, N, K).use && !use_mid(M, N, K);
+}
+
+// The kernels of one MLP call.  kn1 / kn2: the unpacked weights are read as the
+// caller stores them ([K][N]) by the tiled kernels, with no transpose; the other
+// tilings (and the fp16-hidden GEMM2) read transposed copies in the workspace.
+struct MlpPlan {
+    RqPlan rq;
+    bool a16;       // GEMM2 reads the fp16 hidden (INT8K_MLP_GEMM2_FP16_HIDDEN=1)
+    bool kn1, kn2;
+};
+
+MlpPlan mlp_plan(int T, int dm, int dff, int flags) {
+    MlpPlan pl;
+    pl.rq = rq_plan(T, dm, dff, flags);
+    pl.a16 = !pl.rq.g1 && !use_skinny(T, dm, dff) && !splitk_plan(T, dm, dff).use &&
+             gemm2_reads_fp16_hidden();
+    const bool unpacked = (flags & INT8K_MLP_WEIGHTS_PREPACKED) == 0;
+    pl.kn1 = unpacked && tiled_256(T, dff, dm);
+    pl.kn2 = unpacked && !pl.a16 && tiled_256(T, dm, dff);
+    return pl;
+}
+
 // Workspace layout of one MLP call (all offsets 256-byte aligned).
 struct MlpWorkspace {
     int8_t* w1t;      // [d_ff][d_model]  (absent when prepacked)
@@ -1405,7 +1433,8 @@ struct MlpWorkspace {
     size_t bytes;
 };
 
-MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked, const RqPlan& rp) {
+MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked, const MlpPlan& pl) {
+    const RqPlan& rp = pl.rq;
     char* p = static_cast<char*>(base);
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -1415,8 +1444,8 @@ MlpWorkspace carve_mlp(void* base, int T, int dm, int dff, bool prepacked, const
     };
     MlpWorkspace w{};
     const size_t wbytes = prepacked ? 0 : (size_t)dm * dff;
-    w.w1t = reinterpret_cast<int8_t*>(take(wbytes));
-    w.w2t = reinterpret_cast<int8_t*>(take(wbytes));
+    w.w1t = reinterpret_cast<int8_t*>(take(pl.kn1 ? 0 : wbytes));
+    w.w2t = reinterpret_cast<int8_t*>(take(pl.kn2 ? 0 : wbytes));
     w.h16 = reinterpret_cast<uint16_t*>(take(rp.g1 ? 0 : (size_t)T * dff * 2));
     w.hq = reinterpret_cast<int8_t*>(take((size_t)T * dff));
     w.sh = reinterpret_cast<float*>(take((size_t)T * 4));
@@ -1446,12 +1475,14 @@ int configure_lds() {
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)gemm_i8_kernel<EPI_F16>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)gemm_i8_rq_kernel<EPI_GELU_F16>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)gemm_i8_rq_kernel<EPI_F16>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
+        const void* epi_kernels[] = {
+            (const void*)gemm_i8_rq_kernel<EPI_GELU_F16>, (const void*)gemm_i8_rq_kernel<EPI_F16>,
+            (const void*)gemm_i8_rq_kernel<EPI_GELU_F16, true>,
+            (const void*)gemm_i8_rq_kernel<EPI_F16, true>,
+            (const void*)gemm_i8_kernel<EPI_GELU_F16, true>, (const void*)gemm_i8_kernel<EPI_F16, true>};
+        for (const void* k : epi_kernels)
+            if (e == hipSuccess)
+                e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kEpiLdsBytes);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)gemm_i8_a16_kernel,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kA16LdsBytes);
@@ -1500,7 +1531,7 @@ extern "C" int int8k_transpose_int8_weights(const int8_t* W1, const int8_t* W2, 
 extern "C" size_t int8k_mlp_workspace_bytes(int T, int d_model, int d_ff, int flags) {
     if (T <= 0 || d_model <= 0 || d_ff <= 0) return 0;
     return carve_mlp(nullptr, T, d_model, d_ff, (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0,
-                     rq_plan(T, d_model, d_ff, flags))
+                     mlp_plan(T, d_model, d_ff, flags))
         .bytes;
 }
 
@@ -1539,8 +1570,9 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
         return INT8K_ERR_MISALIGNED;
     const bool prepacked = (flags & INT8K_MLP_WEIGHTS_PREPACKED) != 0;
     const bool per_tensor_out = (flags & INT8K_MLP_OUT_PER_TENSOR) != 0;
-    const RqPlan rp = rq_plan(T, d_model, d_ff, flags);
-    const MlpWorkspace w = carve_mlp(workspace, T, d_model, d_ff, prepacked, rp);
+    const MlpPlan pl = mlp_plan(T, d_model, d_ff, flags);
+    const RqPlan& rp = pl.rq;
+    const MlpWorkspace w = carve_mlp(workspace, T, d_model, d_ff, prepacked, pl);
     if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
     if (!aligned_to(workspace, 256)) return INT8K_ERR_MISALIGNED;
     int st = configure_lds();
@@ -1557,12 +1589,16 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
         if ((st = check_launch("rq_clear_kernel")) != INT8K_OK) return st;
     }
 
+    // W1t / W2t: [N][K] operands (prepacked, or transposed here), or the caller's
+    // [K][N] weights themselves where kn1 / kn2 read them as stored
     const int8_t* W1t = W1;
     const int8_t* W2t = W2;
-    if (!prepacked) {
+    if (!prepacked && !pl.kn1) {
         if ((st = launch_transpose(W1, w.w1t, d_model, d_ff, s)) != INT8K_OK) return st;
-        if ((st = launch_transpose(W2, w.w2t, d_ff, d_model, s)) != INT8K_OK) return st;
         W1t = w.w1t;
+    }
+    if (!prepacked && !pl.kn2) {
+        if ((st = launch_transpose(W2, w.w2t, d_ff, d_model, s)) != INT8K_OK) return st;
         W2t = w.w2t;
     }
     // GEMM1 + scale/bias/GELU epilogue -> int8 hidden + row scales (fused requant), or
@@ -1577,9 +1613,14 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     p1.bias = bias1;
     p1.pmax = w.p1;
     const SplitKPlan sk1 = splitk_plan(T, d_ff, d_model);
-    if (rp.g1)
+    if (rp.g1 && pl.kn1)
+        st = launch_gemm_rq<EPI_GELU_F16, true>(x, W1t, T, d_ff, d_model, p1, w.hq, w.sh, amax1,
+                                                arrived1, s);
+    else if (rp.g1)
         st = launch_gemm_rq<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, w.hq, w.sh, amax1,
                                           arrived1, s);
+    else if (pl.kn1)
+        st = launch_gemm<EPI_GELU_F16, true>(x, W1t, T, d_ff, d_model, p1, s);
     else if (use_skinny(T, d_ff, d_model))
         st = launch_gemm_skinny<EPI_GELU_F16>(x, W1t, T, d_ff, d_model, p1, s);
     else if (sk1.use)
@@ -1603,7 +1644,7 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     const SplitKPlan sk2 = splitk_plan(T, d_model, d_ff);
     const bool skinny2 = use_skinny(T, d_model, d_ff);
     // the on-load path has 256 x 256 tiles on every grid it runs
-    const bool a16 = !rp.g1 && !skinny2 && !sk2.use && gemm2_reads_fp16_hidden();
+    const bool a16 = pl.a16;
     if (!rp.g1 && !a16) {
         // per-token requant of the hidden (one absmax partial per row and 256-column
         // tile, or per 32-column block of the skinny path)
@@ -1611,6 +1652,9 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
                                  s)) != INT8K_OK)
             return st;
     }
+    if (rp.g2 && pl.kn2)
+        return launch_gemm_rq<EPI_F16, true>(w.hq, W2t, T, d_model, d_ff, p2, out, out_scale,
+                                             amax2, arrived2, s);
     if (rp.g2)
         return launch_gemm_rq<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, out, out_scale, amax2,
                                        arrived2, s);
@@ -1621,7 +1665,9 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
             w.h16, W2t, T, d_model, d_ff, tiles_m, tiles_n, w.p1, tn1, p2);
         if ((st = check_launch("gemm_i8_a16_kernel")) != INT8K_OK) return st;
     } else {
-        if (skinny2)
+        if (pl.kn2)
+            st = launch_gemm<EPI_F16, true>(w.hq, W2t, T, d_model, d_ff, p2, s);
+        else if (skinny2)
             st = launch_gemm_skinny<EPI_F16>(w.hq, W2t, T, d_model, d_ff, p2, s);
         else if (sk2.use)
             st = launch_gemm_splitk<EPI_F16>(w.hq, W2t, T, d_model, d_ff, sk2, w.part, p2, s);

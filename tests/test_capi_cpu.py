@@ -255,3 +255,14 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_mlp_unpacked_workspace_holds_no_weight_copies(capi):
+    # where both GEMMs run the 256 x 256 kernels, the unpacked weights are read as stored:
+    # the workspace holds no transposed copies; the 128 x 128 GEMM2 of (2048, 2048, 8192)
+    # still reads a transposed W2
+    P = capi.MLP_WEIGHTS_PREPACKED
+    assert capi.mlp_workspace_bytes(4096, 4096, 16384, 0) == capi.mlp_workspace_bytes(
+        4096, 4096, 16384, P)
+    assert capi.mlp_workspace_bytes(2048, 2048, 8192, 0) >= capi.mlp_workspace_bytes(
+        2048, 2048, 8192, P) + 2048 * 8192
