@@ -514,9 +514,10 @@ def bench_decode_paged(args):
 def measure_paged(B, H, D, S, pages, args, dev, stream):
     """Paged decode at one shape for each page size in `pages`: the contiguous case's data
     (same seed) cut into pages stored in a seeded random physical order, one block-table row
-    per sequence, every length = S.  Timed as measure_decode (median of 5 windows; cases
-    under 512 MB cycle through cache copies), with every (b,h) row checked against the C
-    oracle.  The contiguous kernel's line for the same shape and seed sits beside it."""
+    per sequence, every length = S.  Windows of `--steps` paged steps alternate with windows
+    of the contiguous kernel on the same data (5 each, medians reported), so the paging tax
+    is measured under the same clock; cases under 512 MB cycle through cache copies.  Every
+    (b,h) row of the paged output is checked against the C oracle."""
     import ctypes
 
     import numpy as np
@@ -537,6 +538,17 @@ def measure_paged(B, H, D, S, pages, args, dev, stream):
     Pt = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     st = ctypes.c_void_p(stream.cuda_stream)
     kv_bytes = 2 * BH * S * D
+    total = kv_bytes + 2 * BH * S * 4
+    n_copies = 1 if total >= (512 << 20) else max(3, -(-(768 << 20) // total))
+    Q, sQ = case["Qi"], case["sQ"]
+    flat = (case["Ki"].reshape(BH, S, D), case["Vi"].reshape(BH, S, D), case["sK"].reshape(-1),
+            case["sV"].reshape(-1))
+    ccopies = [flat] + [tuple(t.clone() for t in flat) for _ in range(n_copies - 1)]
+    cout = torch.empty((BH, D), dtype=torch.float16, device=dev)
+    cws = torch.empty(max(capi.decode_workspace_bytes(BH, S, D, args.nsplit), 1),
+                      dtype=torch.uint8, device=dev)
+    ccalls = [(Pt(Q), Pt(K), Pt(V), Pt(cout), Pt(sQ), Pt(sK), Pt(sV), BH, S, D, args.nsplit,
+               Pt(cws), cws.numel(), st) for (K, V, sK, sV) in ccopies]
 
     def check(out, what):
         got = out.float().reshape(BH, D).cpu().numpy()
@@ -546,11 +558,23 @@ def measure_paged(B, H, D, S, pages, args, dev, stream):
             raise SystemExit(f"{what} does not match the oracle (max_abs={err}, cos={cos})")
         return {"rows_checked": BH, "max_abs": err, "cos": round(cos, 7)}
 
+    def runner(fn, calls):
+        it = [0]
+
+        def step():
+            a = calls[it[0] % len(calls)]
+            it[0] += 1
+            rc = fn(*a)
+            if rc != 0:
+                capi.check("decode", rc)
+        return step
+
+    cstep = runner(lib.int8k_decode_attention_forward, ccalls)
     rows = []
     for P in pages:
         npp = -(-S // P)
         NP = B * npp
-        perm = torch.randperm(NP, generator=torch.Generator().manual_seed(args.seed + P)).to(dev)
+        perm = torch.randperm(NP, generator=torch.Generator().manual_seed(args.seed)).to(dev)
 
         def to_pages(x):  # [B, H, S, ...] -> [NP, H, P, ...]; page (b, i) at perm[b*npp + i]
             tail = tuple(x.shape[3:])
@@ -561,32 +585,27 @@ def measure_paged(B, H, D, S, pages, args, dev, stream):
             o[perm] = pg
             return o
 
-        cache = (to_pages(case["Ki"]), to_pages(case["Vi"]), to_pages(case["sK"]),
-                 to_pages(case["sV"]))
-        total = kv_bytes + 2 * BH * S * 4
-        n_copies = 1 if total >= (512 << 20) else max(3, -(-(768 << 20) // total))
+        cache = tuple(to_pages(case[k]) for k in ("Ki", "Vi", "sK", "sV"))
         copies = [cache] + [tuple(t.clone() for t in cache) for _ in range(n_copies - 1)]
         tables = perm.to(torch.int32).reshape(B, npp).contiguous()
         lens = torch.full((B,), S, dtype=torch.int32, device=dev)
         out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
         ws = torch.empty(max(capi.decode_paged_workspace_bytes(B, H, S, D, args.nsplit), 1),
                          dtype=torch.uint8, device=dev)
-        calls = [(Pt(case["Qi"]), Pt(Kp), Pt(Vp), Pt(out), Pt(case["sQ"]), Pt(sKp), Pt(sVp),
-                  Pt(tables), Pt(lens), B, H, D, NP, P, npp, S, args.nsplit, Pt(ws), ws.numel(),
-                  st) for (Kp, Vp, sKp, sVp) in copies]
-        it = [0]
-
-        def step():
-            a = calls[it[0] % n_copies]
-            it[0] += 1
-            rc = lib.int8k_decode_attention_forward_paged(*a)
-            if rc != 0:
-                capi.check("int8k_decode_attention_forward_paged", rc)
-
-        ms, windows = time_windows(step, args.steps, max(args.warmup, 2 * n_copies), stream)
+        pstep = runner(lib.int8k_decode_attention_forward_paged,
+                       [(Pt(Q), Pt(Kp), Pt(Vp), Pt(out), Pt(sQ), Pt(sKp), Pt(sVp), Pt(tables),
+                         Pt(lens), B, H, D, NP, P, npp, S, args.nsplit, Pt(ws), ws.numel(), st)
+                        for (Kp, Vp, sKp, sVp) in copies])
+        for _ in range(max(args.warmup, 2 * n_copies)):
+            cstep()
+            pstep()
+        pw, cw = [], []
+        for _ in range(WINDOWS):
+            cw.append(time_steps(cstep, args.steps, 0, stream))
+            pw.append(time_steps(pstep, args.steps, 0, stream))
+        ms, cms = statistics.median(pw), statistics.median(cw)
         out.zero_()
-        it[0] = 0
-        step()
+        pstep()
         torch.cuda.synchronize()
         parity = check(out, f"paged decode B{B} H{H} D{D} S{S} page {P}")
         tbs = kv_bytes / (ms * 1e-3) / 1e12
@@ -594,10 +613,14 @@ def measure_paged(B, H, D, S, pages, args, dev, stream):
                      "nsplit": capi.decode_paged_num_splits(B, H, S, D, args.nsplit),
                      "us": round(ms * 1e3, 2), "TBps": round(tbs, 4),
                      "pct_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS * 100, 2),
-                     "windows_ms": windows, "cache_copies": n_copies, "parity": parity})
+                     "contiguous_us": round(cms * 1e3, 2),
+                     "vs_contiguous": round(ms / cms, 4),
+                     "windows_ms": [round(w, 5) for w in pw], "cache_copies": n_copies,
+                     "parity": parity})
         log(f"[bench] paged decode B{B} H{H} D{D} ctx{S} page {P}: {ms * 1e3:.1f} us "
-            f"{tbs:.3f} TB/s, all {BH} rows vs oracle: max_abs {parity['max_abs']:.1e}")
-        del copies, cache, calls, ws
+            f"{tbs:.3f} TB/s ({ms / cms:.3f}x the contiguous {cms * 1e3:.1f} us in alternate "
+            f"windows), all {BH} rows vs oracle: max_abs {parity['max_abs']:.1e}")
+        del copies, cache, ws
         torch.cuda.empty_cache()
     return rows
 
