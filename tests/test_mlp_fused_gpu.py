@@ -114,3 +114,53 @@ def test_fused_requant_hidden_beyond_fp16_range(gpu):
     torch.cuda.synchronize()
     assert torch.equal(out_f, out_s) and torch.equal(osc_f, osc_s)
     assert capi.mlp_sync_timeouts() == 0
+
+
+def test_fused_requant_under_graph_capture(gpu):
+    # the fused path is kernels only (the counters are cleared by a kernel, not a memset), so
+    # a captured MLP replays; every replay, with eager work on the same workspace between
+    # replays, equals the eager output byte for byte
+    T, dm, dff = 4096, 4096, 16384
+    print("fused requant graph capture", flush=True)
+    c = workloads.mlp_case(T, dm, dff, seed=13, device=gpu)
+    W1T, W2T = capi.transpose_int8_weights(c["W1"], c["W2"])
+    x = c["x"].reshape(T, dm)
+    ws = torch.empty(capi.mlp_workspace_bytes(T, dm, dff, capi.MLP_WEIGHTS_PREPACKED),
+                     dtype=torch.uint8, device=gpu)
+    out = torch.empty(T, dm, dtype=torch.int8, device=gpu)
+    osc = torch.empty(T, dtype=torch.float32, device=gpu)
+    args = (x, W1T, W2T, c["sx"], c["sW1"], c["sW2"])
+    kw = dict(flags=capi.MLP_WEIGHTS_PREPACKED, out=out, out_scale=osc, workspace=ws)
+    capi.mlp_forward(*args, **kw)
+    torch.cuda.synchronize()
+    ref, rsc = out.clone(), osc.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capi.mlp_forward(*args, **kw)
+    other = workloads.mlp_case(T, dm, dff, seed=14, device=gpu)
+    for i in range(3):
+        out.fill_(0)
+        osc.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(osc, rsc), f"replay {i}"
+        # eager work between replays leaves the workspace's counters and maxima dirty
+        capi.mlp_forward(other["x"].reshape(T, dm), W1T, W2T, other["sx"], c["sW1"], c["sW2"],
+                         flags=capi.MLP_WEIGHTS_PREPACKED, workspace=ws)
+        torch.cuda.synchronize()
+    assert capi.mlp_sync_timeouts() == 0
+
+
+def test_fused_requant_dirty_workspace(gpu):
+    # a workspace full of arbitrary bytes (as from the caching allocator) gives the same output
+    T, dm, dff = 2048, 2048, 8192
+    print("fused requant dirty workspace", flush=True)
+    c = workloads.mlp_case(T, dm, dff, seed=21, device=gpu)
+    args = (c["x"].reshape(T, dm), c["W1"], c["W2"], c["sx"], c["sW1"], c["sW2"])
+    ref, rsc = capi.mlp_forward(*args)
+    n = capi.mlp_workspace_bytes(T, dm, dff)
+    for fill in (0xFF, 0x7F, 0xA5):
+        ws = torch.full((n,), fill, dtype=torch.uint8, device=gpu)
+        out, osc = capi.mlp_forward(*args, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(osc, rsc), hex(fill)
