@@ -711,7 +711,17 @@ __global__ __launch_bounds__(64 * MAXW) void decode_paged_block_kernel(
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
-    const int bh = blockIdx.x;
+    // With 16-token pages a head's scales in a page are 64 bytes, and heads 2k
+    // and 2k+1 share one 128-byte line.  Blocks go to the 8 XCDs in turn, so
+    // with 16 | gridDim.x block i of XCD x takes head pair 8 (i / 2) + x: the
+    // pair's two heads run at adjacent slots of one XCD (one L2) and walk their
+    // pages in the same order (one stagger), and the line is fetched once.
+    const bool pair = log2_page < 5 && (gridDim.x & 15) == 0;
+    int bh = blockIdx.x;
+    if (pair) {
+        const int x = bh & 7, i = bh >> 3;
+        bh = ((((i >> 1) << 3) + x) << 1) + (i & 1);
+    }
     const int b = bh / H, hh = bh - b * H;
     const int page = 1 << log2_page;
     const int32_t* table = block_tables + (size_t)b * max_pages;
@@ -735,7 +745,7 @@ __global__ __launch_bounds__(64 * MAXW) void decode_paged_block_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     const int n_full = max(0, j1 - j0) / G::kRowsPerIter;
-    const unsigned unit = (unsigned)bh * (unsigned)nw + (unsigned)w;
+    const unsigned unit = (unsigned)(pair ? bh >> 1 : bh) * (unsigned)nw + (unsigned)w;
     const int it = stagger ? (int)((unit * 2654435761u) >> 16) % max(n_full, 1) : 0;
     // a group's rows (NS-aligned, or the 8-aligned pair block) share one page
     constexpr bool PAIRED = paired_rows(D, NS, MAXW);

@@ -37,6 +37,23 @@ def test_paged_decode_matches_oracle(gpu, D, page):
     assert_attn_close(out.float().cpu().numpy(), _oracle(c))
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,H", [(4, 8), (16, 3)])
+def test_paged_decode_head_pairs(gpu, D, B, H):
+    # 16-token pages with 16 | B*H: the one-launch kernel runs heads 2k and 2k+1 side by
+    # side on one XCD (they share each page's scale line); with H = 3 a pair spans two
+    # sequences with different page tables and lengths
+    rng = np.random.default_rng(B * H + D)
+    lens = [int(v) for v in rng.integers(1, 3000, size=B)]
+    c = workloads.paged_case(B, H, D, 16, lens, seed=B + H + D, device=gpu)
+    out = capi.decode_attention_paged(c["Qi"], c["K_pages"], c["V_pages"], c["sQ"],
+                                      c["sK_pages"], c["sV_pages"], c["block_tables"],
+                                      c["context_lens"], c["max_context"], nsplit=8)
+    torch.cuda.synchronize()
+    assert capi.decode_paged_num_splits(B, H, c["max_context"], D, 8) <= 8  # one launch
+    assert_attn_close(out.float().cpu().numpy(), _oracle(c))
+
+
 def test_paged_decode_via_torch_op(ext, gpu):
     lens = [300, 5, 4096]
     c = workloads.paged_case(3, 8, 128, 16, lens, seed=9, device=gpu)
