@@ -17,7 +17,10 @@ The default run (`--workload all`) measures every BASELINE configuration:
     end-to-end pre-LN block, INT8 against FP16 (block.py).
 Every figure is the median of 5 windows of `--steps` steps after `--warmup`
 untimed steps, timed with HIP events on the launch stream; every config has
-its own `roofline` and an oracle parity check (all rows for decode).
+its own `roofline` and an oracle parity check (all rows for decode).  Decode
+steps shorter than 50 us also report `graph_us`: the same steps captured in a
+HIP graph and replayed, the device time per step without the host's per-call
+issue (config 1's step is otherwise set by one ctypes call and one launch).
 `cpu_baseline` times this repo's torch-CPU fp32 restatement of the reference's
 CPU path (dequantize, then common/baseline.py's math) on a bounded sample of
 the same workload on this host.  Prints ONE JSON line; details go to stderr.
@@ -64,6 +67,30 @@ def time_steps(fn, steps, warmup, stream):
 
 
 WINDOWS = 5
+GRAPH_BELOW_MS = 0.05  # decode steps shorter than this are also timed from a captured graph
+
+
+def time_graph(step_on, n_steps, stream, windows=WINDOWS):
+    """Device time per step with the host's launch issue taken out: `n_steps` steps are
+    captured in one HIP graph (step_on(handle) returns a step that launches on the stream
+    with that handle, here the capture stream) and the graph is replayed in `windows` timed
+    windows on `stream`.  Returns the median window's ms per step."""
+    import ctypes
+
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(stream)
+    with torch.cuda.graph(graph, stream=cap):
+        fn = step_on(ctypes.c_void_p(cap.cuda_stream))
+        for _ in range(n_steps):
+            fn()
+    torch.cuda.synchronize()
+    graph.replay()
+    runs = [time_steps(graph.replay, 1, 0, stream) / n_steps for _ in range(windows)]
+    del graph
+    return statistics.median(runs)
 
 
 def time_windows(fn, steps, warmup, stream, windows=WINDOWS):
@@ -263,19 +290,25 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
     fn = capi.load().int8k_decode_attention_forward
     Pt = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     st = ctypes.c_void_p(stream.cuda_stream)
-    calls = [(Pt(Q), Pt(K), Pt(V), Pt(out), Pt(sQ), Pt(sK), Pt(sV), BH, S, D, args.nsplit,
-              Pt(ws), ws.numel(), st) for (K, V, sK, sV) in copies]
-    it = [0]
+    def step_on(handle):
+        calls = [(Pt(Q), Pt(K), Pt(V), Pt(out), Pt(sQ), Pt(sK), Pt(sV), BH, S, D, args.nsplit,
+                  Pt(ws), ws.numel(), handle) for (K, V, sK, sV) in copies]
+        it = [0]
 
-    def step():
-        a = calls[it[0] % n_copies]
-        it[0] += 1
-        rc = fn(*a)
-        if rc != 0:
-            capi.check("int8k_decode_attention_forward", rc)
+        def step():
+            a = calls[it[0] % n_copies]
+            it[0] += 1
+            rc = fn(*a)
+            if rc != 0:
+                capi.check("int8k_decode_attention_forward", rc)
+        return step
 
     # every cache copy is touched before the first timed window
-    ms, windows = time_windows(step, args.steps, max(args.warmup, 2 * n_copies), stream)
+    ms, windows = time_windows(step_on(st), args.steps, max(args.warmup, 2 * n_copies), stream)
+    # a short step can be set by the host's issue rate (one ctypes call and one launch per
+    # step): its device time is also taken from a captured graph of steps over the copies
+    graph_ms = (time_graph(step_on, n_copies * max(1, 40 // n_copies), stream)
+                if ms < GRAPH_BELOW_MS else None)
     K, V, sK, sV = kv
     out.zero_()
     capi.decode_attention(Q, K, V, sQ, sK, sV, nsplit=args.nsplit, out=out, workspace=ws)
@@ -296,9 +329,14 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
            "pct_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS * 100, 2),
            "windows_ms": windows, "cache_copies": n_copies,
            "parity": {"rows_checked": BH, "max_abs": err, "cos": round(cos, 7)}}
+    if graph_ms is not None:
+        row["graph_us"] = round(graph_ms * 1e3, 2)
+        row["graph_pct_hbm_peak"] = round(kv_bytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS * 100,
+                                          2)
     log(f"[bench] decode B{B} H{H} D{D} ctx{S}: {ms * 1e3:.1f} us {tbs:.3f} TB/s "
         f"({row['pct_hbm_peak']:.1f}% of 8 TB/s), {n_copies} cache copies, "
-        f"all {BH} rows vs oracle: max_abs {err:.1e} cos {cos:.6f}")
+        f"all {BH} rows vs oracle: max_abs {err:.1e} cos {cos:.6f}"
+        + (f"; from a captured graph {graph_ms * 1e3:.1f} us per step" if graph_ms else ""))
     return row, (host if keep_host else None), (out if keep_host else None)
 
 
