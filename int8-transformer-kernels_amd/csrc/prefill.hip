@@ -10,8 +10,8 @@
 //
 // Design (CDNA4): a block owns the queries of one (b,h), 32 per wave (256
 // queries on 8 waves at head_dim 128, 128 queries on 4 waves at 64 and 256),
-// and walks the KV sequence in tiles of 64 keys.  K (int8 rows), V (as fp16
-// V^T) and both key-scale vectors of a tile are staged in double-buffered LDS
+// and walks the KV sequence in tiles of 64 keys.  K (int8 rows), V (fp16,
+// row-major) and both key-scale vectors of a tile are staged in double-buffered LDS
 // by buffer loads: the next tile's loads are in flight in registers while the
 // current tile is computed, and there is one barrier per tile.  The LDS reads
 // of the MFMA fragments and key scales are scheduled ahead of their uses.  The
@@ -25,9 +25,9 @@
 // 16 of the 32 keys, so the row max, the exponentials, the running sum and the
 // rescale of O are lane-local except for one exchange with lane l^32, which
 // holds the other 16 keys of the same query.  P^T feeds the PV MFMA from the
-// registers it was computed in; V is staged once per tile into LDS as fp16 V^T
-// with the key order permuted to match those P^T registers, so each V^T
-// fragment is a single 16-byte LDS read.
+// registers it was computed in; V is staged once per tile into LDS as fp16
+// [key][dim] rows, as it arrives, and each V^T fragment is two transposing LDS
+// reads (ds_read_b64_tr_b16) whose key order matches those P^T registers.
 //
 // Head dims: 64, 128 and 256 run the kernel at their own size; any other
 // multiple of 16 up to 256 runs the next of those sizes with the missing dims
@@ -65,43 +65,47 @@ struct Shape {
     static constexpr int kQ = 32 * kWaves;  // queries per block
     static constexpr int kMinBlocks = D == 64 ? 2 : 1;  // 2 waves per SIMD at D <= 128
 };
-constexpr int kVtStride = kKV + 8;  // fp16 elements per V^T row in LDS (144 B)
-// The V scales are applied once per staged tile, V^T = fp16(v * sV * 2^-E), and
+// The V scales are applied once per staged tile, V' = fp16(v * sV * 2^-E), and
 // the probabilities enter the PV MFMA as P = fp16(p * 2^E), so
-// P . V^T = sum_j p_j v_j sV_j as the reference's fp16(p * sV) . fp16(v)
+// P . V' = sum_j p_j v_j sV_j as the reference's fp16(p * sV) . fp16(v)
 // (kernels/int8_attention.cu:530-572).  E >= 0 is chosen per block, from
 // max|sV| over the keys that block reads ([0, kv_end)), so that
-// 127 * max|sV| * 2^-E <= 32768 (0 for V from fp16 data) and V^T is finite
+// 127 * max|sV| * 2^-E <= 32768 (0 for V from fp16 data) and V' is finite
 // wherever the reference's P' is; E <= kMaxVExp.  Causal query tiles of one
 // (b,h) may use different E: each normalises with its own 2^E.
 constexpr int kMaxVExp = 11;
 
-// LDS position of key kk (0..63) of a tile inside a V^T row: keys
-// 16t + 8a + 4h + c are stored at 16t + 8h + 4a + c, so the 8 keys that lane
-// half h of the PV B-operand holds for slice t are contiguous.
-__device__ __forceinline__ int vt_pos(int kk) {
-    const int t = kk >> 4, a = (kk >> 3) & 1, h = (kk >> 2) & 1, c = kk & 3;
-    return 16 * t + 8 * h + 4 * a + c;
-}
+// V' is staged as it arrives, row-major fp16 [key][dim], and the PV MFMA's
+// V^T fragments are formed by transposing LDS reads (ds_read_b64_tr_b16).
+// Measured on the box: in each group of 16 lanes, the instruction gives lane
+// 4h + e half e of the 8-byte rows that lanes h, h+4, h+8, h+12 address.  So
+// lane 16G + 4k + h of a wave addresses key row 4 (G/2) + k and dims
+// 16 (G%2) + 4h of a 16-key slice, and lane l then holds dim l % 32 of keys
+// 4 (l/32) + 0..3: the first half of its fragment; a read 8 rows further
+// gives the second (see tile_pv).  Rows hold D + 32 halfs (2D + 64 bytes, 64
+// or 192 mod 256), so the 4 rows a half-wave reads fall in 4 different 64-byte
+// bank groups.
+//
+// Work item n of thread t is the 4x4 block of keys 4 kg .. 4 kg + 3 and dims
+// 4 dg .. 4 dg + 3 with kg = t / W, dg = t % W + n W, where W = D / 4 / items
+// per thread (32 at D = 128, 16 at D = 64 and 256): dim groups run fastest, so
+// a wave's loads of one key cover whole 64- or 128-byte runs of rows in memory
+// and its LDS writes whole runs of staged rows, and a thread's items share
+// their keys (one sV vector).
+template <int D>
+struct VLayout {
+    static constexpr int kRow = D + 32;  // halfs per staged row
+    static constexpr int kItems = 64 * D / 16 / Shape<D>::kThreads;
+    static constexpr int kW = D / 4 / kItems;  // dim groups per item row
+};
 
-// Work item it of a V tile is the 4x4 block of keys 4 kg .. 4 kg + 3 and dims
-// 4 dg .. 4 dg + 3.  Key groups run fastest, so the 16 lanes that write one
-// V^T row (8 bytes each) fill it contiguously; the four 16-lane groups of a
-// wave take dim groups +0, +2, +1, +3, so the two groups that share an LDS
-// cycle write rows 8 apart (288 words: the other half of 64 banks).
-__device__ __forceinline__ int v_key_group(int it) { return it & 15; }
-__device__ __forceinline__ int v_dim_group(int it) {
-    const int g = (it >> 4) & 3;
-    return 4 * (it >> 6) + ((g & 1) << 1 | (g >> 1));
-}
-
-// One LDS stage: K tile (int8 rows, 16-byte padded), V^T tile (fp16, the V
-// scales applied), the key scales sK.
+// One LDS stage: K tile (int8 rows, 16-byte padded), V' tile (fp16 [key][dim],
+// the V scales applied), the key scales sK.
 template <int D>
 struct Stage {
     static constexpr int kKStride = D + 16;  // bytes per K row
     static constexpr int kKBytes = kKV * kKStride;
-    static constexpr int kVtBytes = D * kVtStride * 2;
+    static constexpr int kVtBytes = kKV * VLayout<D>::kRow * 2;
     static constexpr int kBytes = kKBytes + kVtBytes + kKV * 4;
     static constexpr int kKChunks = kKV * D / 16 / Shape<D>::kThreads;  // 16-B K chunks per thread
     static constexpr int kVItems = kKV * D / 16 / Shape<D>::kThreads;   // 4x4 V blocks per thread
@@ -113,14 +117,14 @@ struct Stage {
 // as zero, so the tile loads need no clamping; masked keys never reach the
 // output.  `dm` is the head_dim of the rows in memory; a padded kernel
 // (dm < D) loads only the K chunks and V dim groups below dm and zeroes the
-// rest (kvalid, vvalid: bit n for item n).
+// rest (kvalid, vvalid).
 struct TileSrc {
     __amdgpu_buffer_rsrc_t k, s, sv;
     v4i v;  // V descriptor with a typed format: 8_8_8_8 SSCALED (see load_v_f16x4)
     uint32_t voff_k, voff_v, voff_s, voff_sv;
     uint32_t kstep, dm;  // bytes between K chunks n and n+1; row stride in memory
     bool kvalid;
-    uint32_t vvalid;
+    uint32_t vvalid;  // bit n: item n has dims below dm
 };
 
 // A buffer descriptor whose loads convert: data format 8_8_8_8 with numeric
@@ -173,13 +177,15 @@ __device__ __forceinline__ TileSrc make_tile_src(const int8_t* Kbh, const int8_t
     src.voff_k = (t / (D / 16)) * dm + kcol;
     src.kstep = (uint32_t)(kT * 16 / D) * dm;  // chunk t + n kT is kT*16/D rows further
     src.kvalid = kcol < dm;
-    src.voff_v = 4 * v_key_group(t) * dm + 4 * v_dim_group(t);
+    using VL = VLayout<D>;
+    const int dg = t % VL::kW, kg = t / VL::kW;
+    src.voff_v = 4 * kg * dm + 4 * dg;
     src.vvalid = 0;
 #pragma unroll
-    for (int n = 0; n < Stage<D>::kVItems; ++n)
-        if (4 * v_dim_group(t + n * kT) < dm) src.vvalid |= 1u << n;
+    for (int n = 0; n < VL::kItems; ++n)
+        if (4 * (dg + n * VL::kW) < dm) src.vvalid |= 1u << n;
     src.voff_s = (t & (kKV - 1)) * 4;
-    src.voff_sv = 4 * v_key_group(t) * 4;
+    src.voff_sv = 16 * kg;
     return src;
 }
 
@@ -188,18 +194,19 @@ template <int D>
 struct Prefetch {
     int4 k[Stage<D>::kKChunks];
     uint2 v[Stage<D>::kVItems][4];  // key 4 kg + i, dims 4 dg .. 4 dg + 3 as fp16 pairs
-    float4 sv;  // sV of keys 4 kg .. 4 kg + 3 (the same for every V item of a thread)
+    float4 sv;  // sV of keys 4 kg .. 4 kg + 3 (the keys of every item of the thread)
     float sc;   // threads 0..63: sK of key tid
 };
 
 // Thread t (of kT) loads 16-byte K chunk t + kT n (row (t + kT n) / (D/16);
-// chunks of consecutive n are kT*16/D rows apart) and the 4x4 int8 V block
-// t + kT n (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3; blocks of
-// consecutive n are kT/16 dim groups = kT/4 bytes apart).  PAD: chunks and
-// blocks past the memory head_dim are zero.
+// chunks of consecutive n are kT*16/D rows apart), the 4x4 int8 V blocks of its
+// items (rows 4 kg .. 4 kg + 3, dims 4 dg .. 4 dg + 3; items n and n+1 are
+// 4 VLayout::kW bytes apart) and their 4 sV.  PAD: chunks and blocks past the
+// memory head_dim are zero.
 template <int D, bool PAD>
 __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& src, int k0) {
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    typedef float v4f __attribute__((ext_vector_type(4)));
     constexpr int kT = Shape<D>::kThreads;
     const uint32_t dm = PAD ? src.dm : (uint32_t)D;
 #pragma unroll
@@ -217,13 +224,13 @@ __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& sr
         if (!PAD || (src.vvalid >> n) & 1u) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                pf.v[n][i] = load_v_f16x4(src.v, src.voff_v, k0 * dm + n * (kT / 4) + i * dm);
+                pf.v[n][i] = load_v_f16x4(src.v, src.voff_v,
+                                          (k0 + i) * dm + n * 4 * VLayout<D>::kW);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) pf.v[n][i] = make_uint2(0, 0);
         }
     }
-    typedef float v4f __attribute__((ext_vector_type(4)));
     const v4f sv = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(src.sv, src.voff_sv,
                                                                                 k0 * 4, 0));
     pf.sv = make_float4(sv.x, sv.y, sv.z, sv.w);
@@ -232,10 +239,12 @@ __device__ __forceinline__ void prefetch_tile(Prefetch<D>& pf, const TileSrc& sr
                                                                                k0 * 4, 0));
 }
 
-// vscale = 2^-E: V^T = fp16(v * fp16(sV * 2^-E)) on v_pk_mul_f16.
+// vscale = 2^-E: V' = fp16(v * fp16(sV * 2^-E)) on v_pk_mul_f16, written as it
+// arrived: each key's 4 dims of an item as one 8-byte row piece.
 template <int D>
 __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st, float vscale) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    using VL = VLayout<D>;
     const int t = threadIdx.x;
 #pragma unroll
     for (int n = 0; n < Stage<D>::kKChunks; ++n) {
@@ -243,37 +252,21 @@ __device__ __forceinline__ void commit_tile(const Prefetch<D>& pf, char* st, flo
         const int row = c / (D / 16), col = (c % (D / 16)) * 16;
         *reinterpret_cast<int4*>(st + row * Stage<D>::kKStride + col) = pf.k[n];
     }
-    _Float16* vt = reinterpret_cast<_Float16*>(st + Stage<D>::kKBytes);
-    // fp16 pair {key a, key b} of one dim from the two keys' {d, d+1} words
-    constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;
+    _Float16* vs = reinterpret_cast<_Float16*>(st + Stage<D>::kKBytes) +
+                   (t / VL::kW) * 4 * VL::kRow + (t % VL::kW) * 4;
+    // key 4 kg + i scaled by its sV * 2^-E (both dims of a word share the key)
+    const float svk[4] = {pf.sv.x * vscale, pf.sv.y * vscale, pf.sv.z * vscale,
+                          pf.sv.w * vscale};
 #pragma unroll
-    for (int n = 0; n < Stage<D>::kVItems; ++n) {
-        const int it = t + n * Shape<D>::kThreads;
-        const int kg = v_key_group(it), dg = v_dim_group(it);
-        const int p0 = vt_pos(4 * kg);
-        // key 4 kg + i scaled by its sV * 2^-E (both dims of a word share the key)
-        const float svk[4] = {pf.sv.x * vscale, pf.sv.y * vscale, pf.sv.z * vscale,
-                              pf.sv.w * vscale};
-        uint2 w[4];
+    for (int i = 0; i < 4; ++i) {
+        const h2 sp = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){svk[i], svk[i]}, h2);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const h2 sp = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){svk[i], svk[i]}, h2);
-            w[i].x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pf.v[n][i].x) * sp);
-            w[i].y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pf.v[n][i].y) * sp);
+        for (int n = 0; n < Stage<D>::kVItems; ++n) {
+            uint2 w;
+            w.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pf.v[n][i].x) * sp);
+            w.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pf.v[n][i].y) * sp);
+            *reinterpret_cast<uint2*>(vs + i * VL::kRow + n * 4 * VL::kW) = w;
         }
-        // dim 4 dg + j of keys 4 kg .. 4 kg + 3 -> 4 consecutive fp16 of V^T row 4 dg + j
-        *reinterpret_cast<uint2*>(vt + (4 * dg + 0) * kVtStride + p0) =
-            make_uint2(__builtin_amdgcn_perm(w[1].x, w[0].x, kLo),
-                       __builtin_amdgcn_perm(w[3].x, w[2].x, kLo));
-        *reinterpret_cast<uint2*>(vt + (4 * dg + 1) * kVtStride + p0) =
-            make_uint2(__builtin_amdgcn_perm(w[1].x, w[0].x, kHi),
-                       __builtin_amdgcn_perm(w[3].x, w[2].x, kHi));
-        *reinterpret_cast<uint2*>(vt + (4 * dg + 2) * kVtStride + p0) =
-            make_uint2(__builtin_amdgcn_perm(w[1].y, w[0].y, kLo),
-                       __builtin_amdgcn_perm(w[3].y, w[2].y, kLo));
-        *reinterpret_cast<uint2*>(vt + (4 * dg + 3) * kVtStride + p0) =
-            make_uint2(__builtin_amdgcn_perm(w[1].y, w[0].y, kHi),
-                       __builtin_amdgcn_perm(w[3].y, w[2].y, kHi));
     }
     if (t < kKV) reinterpret_cast<float*>(st + Stage<D>::kKBytes + Stage<D>::kVtBytes)[t] = pf.sc;
 }
@@ -439,15 +432,27 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
                 sacc[T] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[s], qf[s], sacc[T], 0, 0, 0);
         }
     };
-    // O^T += V^T . P^T
+    // O^T += V^T . P^T; the V^T fragment of dim slice t and 16-key slice ks is two
+    // transposing reads of the row-major V' (VLayout): keys 16 ks + 4 (lane/32) + 0..3,
+    // then 8 keys further, at dim 32 t + lane % 32
+    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
+    constexpr int kVRowB = 2 * VLayout<D>::kRow;  // bytes per staged V' row
+    const int v_lane = (4 * (lane >> 5) + ((lane & 15) >> 2)) * kVRowB +
+                       2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3));
     auto pv = [&](int kt, const v8h (&pfr)[4]) {
-        const _Float16* vt = reinterpret_cast<const _Float16*>(stage_of(kt) + St::kKBytes);
+        const char* vs = stage_of(kt) + St::kKBytes + v_lane;
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
-            const _Float16* row = vt + (32 * t + (lane & 31)) * kVtStride + 8 * h;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const v8h vf = *reinterpret_cast<const v8h*>(row + 16 * ks);
+                const char* p = vs + 16 * ks * kVRowB + 64 * t;
+                const v4h lo = __builtin_bit_cast(
+                    v4h, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p));
+                const v4h hi = __builtin_bit_cast(
+                    v4h, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p + 8 * kVRowB)));
+                const v8h vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pfr[ks], o[t], 0, 0, 0);
             }
         }
@@ -473,14 +478,14 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     };
-    // V^T fragments 4 MFMAs ahead of their use
+    // V^T fragments (two reads each) 4 MFMAs ahead of their use
     auto schedule_pv = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
         for (int i = 0; i < 4 * NS - 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     };
