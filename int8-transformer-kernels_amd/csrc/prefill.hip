@@ -354,12 +354,20 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     const int kv_end = CAUSAL ? q_block_end : S;
     const int n_kv = (kv_end + kKV - 1) / kKV;
     const int q_wave_last = min(qw0 + 31, S - 1);
+    // Step i of the KV walk computes tile tile_of(i).  Causal blocks take their
+    // diagonal tiles first (tiles kd .. n_kv-1, the ones some query of the block
+    // does not see whole, which take the slow path anyway), so the running max is
+    // set when the unmasked tiles 0 .. kd-1 follow on the fast path; otherwise the
+    // first of those would take the slow path only to set it.
+    const int kd = CAUSAL ? (qt * kQ) / kKV : 0;
+    const int nd = n_kv - kd;
+    auto tile_of = [&](int i) { return CAUSAL ? (i < nd ? kd + i : i - nd) : i; };
 
     // The first tile's loads go out before the exponent's reduction, so their
     // latency overlaps it.
     const TileSrc src = make_tile_src<D>(Kbh, Vbh, sKbh, sVbh, S, dm);
     Prefetch<D> pa;
-    prefetch_tile<D, PAD>(pa, src, 0);
+    prefetch_tile<D, PAD>(pa, src, tile_of(0) * kKV);
 
     // E: the exponent that keeps the scaled V^T in fp16 range, from max |sV| over
     // the keys this block reads (a block-wide reduction through LDS).  Each thread
@@ -460,8 +468,8 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     auto sk_of = [&](int kt) {
         return reinterpret_cast<const float*>(stage_of(kt) + St::kKBytes + St::kVtBytes);
     };
-    // A wave computes tile kt unless the causal mask hides all of it from the wave's queries.
-    auto computes = [&](int kt) { return !(CAUSAL && kt * kKV > q_wave_last); };
+    // A wave computes tile k unless the causal mask hides all of it from the wave's queries.
+    auto computes = [&](int k) { return !(CAUSAL && k * kKV > q_wave_last); };
     // Keep the K-fragment and sK reads of the fast tile ahead of their uses
     // (the compiler otherwise waits on each LDS read right before its MFMA).
     auto schedule_qk = [&]() {
@@ -498,36 +506,38 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
     // >= 0: p = 2^(u*qscale - m + E) with the current m, no per-score max and no
     // rescale of O; the tile is kept if each lane's sum of its 32 P stays below the
     // fp16 maximum, so every P is finite.  p may exceed 1 when the scores have grown
-    // since m was set; O and l hold such values in fp32.  Every other tile (first
-    // tile, masked edge and diagonal tiles, a sum past the fp16 range) takes the slow
-    // path, which sets m to the exact running max and rescales O and l.  l sums the
-    // fp16 P that enter the PV product.
+    // since m was set; O and l hold such values in fp32.  Every other tile (the
+    // wave's first, masked edge and diagonal tiles, a sum past the fp16 range) takes
+    // the slow path, which sets m to the exact running max and rescales O and l.  l
+    // sums the fp16 P that enter the PV product.
     //
-    // Tile kt is computed from LDS stage kt&1.  The register set holds tile
-    // kt+1 while tile kt is computed; at the end of the step it is written to
-    // the other stage, refilled with tile kt+2, and the step's one barrier
-    // follows.  The fast path runs as an inner loop that the slow path leaves
-    // and re-enters, so O has no conditional update inside it.
+    // Step kt is computed from LDS stage kt&1.  The register set holds step
+    // kt+1's tile while step kt is computed; at the end of the step it is written
+    // to the other stage, refilled with step kt+2's tile, and the step's one
+    // barrier follows.  The fast path runs as an inner loop that the slow path
+    // leaves and re-enters, so O has no conditional update inside it.
     commit_tile<D>(pa, smem, vscale);
-    if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, kKV);
+    if (n_kv > 1) prefetch_tile<D, PAD>(pa, src, tile_of(1) * kKV);
     __syncthreads();
     auto advance = [&](int kt) {
         if (kt + 1 < n_kv) {
             commit_tile<D>(pa, smem + ((kt + 1) & 1) * St::kBytes, vscale);
-            if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pa, src, (kt + 2) * kKV);
+            if (kt + 2 < n_kv) prefetch_tile<D, PAD>(pa, src, tile_of(kt + 2) * kKV);
         }
-        // tile kt+1 is in LDS and every wave is done reading stage kt&1
+        // step kt+1's tile is in LDS and every wave is done reading stage kt&1
         __syncthreads();
     };
+    bool have_m = false;  // wave-uniform: a slow step has set the running max
     int kt = 0;
     while (kt < n_kv) {
         v16i sacc[2];
         bool slow = false;
         for (; kt < n_kv; ++kt) {
-            if (computes(kt)) {
-                const int k0 = kt * kKV;
+            const int tk = tile_of(kt);
+            if (computes(tk)) {
+                const int k0 = tk * kKV;
                 const bool full = k0 + kKV <= S && !(CAUSAL && k0 + kKV - 1 > qw0);
-                if (!(full && qpos)) {
+                if (!(full && qpos && have_m)) {
                     qk(kt, sacc);
                     slow = true;
                     break;
@@ -559,10 +569,10 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
             advance(kt);
         }
         if (!slow) break;
-        // Slow path for tile kt (its S^T is in sacc): s = acc * qscale * sK with masked
+        // Slow path for step kt (its S^T is in sacc): s = acc * qscale * sK with masked
         // keys at -inf, exact running max, rescale of O and l.
         {
-            const int k0 = kt * kKV;
+            const int k0 = tile_of(kt) * kKV;
             const float* sk_l = sk_of(kt);
             float sc[2][16];
             float mx = -INFINITY;
@@ -604,6 +614,7 @@ __global__ __launch_bounds__(Shape<D>::kThreads, Shape<D>::kMinBlocks) void pref
             lsum += psum(pfr);
             pv(kt, pfr);
         }
+        have_m = true;
         advance(kt);
         ++kt;
     }
