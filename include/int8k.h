@@ -147,7 +147,8 @@ int int8k_decode_attention_forward_cache_quant(
  * positions.  page_size must be a power of two in [16, 1024];
  * max_context <= max_pages_per_seq * page_size.  A page id outside
  * [0, num_pages) reads page num_pages-1, so a corrupt table reads wrong pages
- * rather than memory outside the cache.  nsplit as for the contiguous call, planned on
+ * rather than memory outside the cache, and is counted (see
+ * int8k_decode_paged_bad_page_ids).  nsplit as for the contiguous call, planned on
  * max_context; the workspace comes from
  * int8k_decode_attention_paged_workspace_bytes. */
 size_t int8k_decode_attention_paged_workspace_bytes(int B, int H, int max_context,
@@ -165,6 +166,15 @@ int int8k_decode_attention_forward_paged(
     const int32_t* block_tables, const int32_t* context_lens,
     int B, int H, int head_dim, int num_pages, int page_size, int max_pages_per_seq,
     int max_context, int nsplit, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Diagnostics of the paged calls: *count receives how many work units, on the
+ * current device since the library was loaded, met a page id outside
+ * [0, num_pages) among the table entries their positions use (entries past a
+ * sequence's length are never read and never counted).  A unit is a (b, h) for
+ * plans of up to 8 chunks and a (b, h, chunk) for larger ones, so one bad entry
+ * counts at least once per head of its sequence.  Synchronises with the device.
+ * No counterpart in the reference, whose decode has no page table. */
+int int8k_decode_paged_bad_page_ids(unsigned int* count);
 
 /* int8 rows (out_q [B, H, D], out_scale [B*H]) from the paged decode; see
  * int8k_decode_attention_forward_quant. */

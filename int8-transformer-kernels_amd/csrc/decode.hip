@@ -102,6 +102,11 @@ constexpr int kMaxBlockSplits = 16;
 // register sets, paired rows at D=64) measured 2-27% faster at every shape
 // tried (B1 H12 D64 1K to B16 H32 D128 8K).  Forced split counts still may.
 constexpr int kMaxAutoBlockSplits = 8;
+// Work units (a (b,h) of a one-launch plan, a (b,h,chunk) of a split plan) that
+// met a page id outside [0, num_pages) among the pages their positions use
+// (int8k_decode_paged_bad_page_ids).  Such an id reads the last page instead.
+__device__ unsigned int g_paged_bad_ids;
+
 // Largest page-id table the paged one-launch kernel stages in LDS (12288 ids);
 // longer tables run the paged split + combine pair.
 constexpr long long kPagedLdsTableBytes = 48 << 10;
@@ -725,10 +730,16 @@ __global__ __launch_bounds__(64 * MAXW) void decode_paged_block_kernel(
     const int b = bh / H, hh = bh - b * H;
     const int page = 1 << log2_page;
     const int32_t* table = block_tables + (size_t)b * max_pages;
-    for (int i = threadIdx.x; i < n_tab; i += blockDim.x)
-        s_pages[i] = (int)min((unsigned)table[i], (unsigned)(num_pages - 1));
-    __syncthreads();
     const int len = min(context_lens[b], n_tab << log2_page);
+    const int used = (len + page - 1) >> log2_page;  // entries past it are never read
+    bool bad = false;
+    for (int i = threadIdx.x; i < n_tab; i += blockDim.x) {
+        const int id = table[i];
+        bad |= i < used && (unsigned)id >= (unsigned)num_pages;
+        s_pages[i] = (int)min((unsigned)id, (unsigned)(num_pages - 1));
+    }
+    if (__syncthreads_or(bad) && threadIdx.x == 0)
+        __hip_atomic_fetch_add(&g_paged_bad_ids, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int j0 = w * chunk;
     const int j1 = min(len, j0 + chunk);
     const int sub = lane % LPR;
@@ -807,9 +818,13 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
     const Int4 q = load16(Q + (size_t)bh * D + sub * 16);
     const float qscale = sQ[bh] * qk_scale_log2;
     const int32_t* table = block_tables + (size_t)b * max_pages;
-    // element offset of row r of this head (an id outside [0, num_pages) reads the last page)
+    // element offset of row r of this head (an id outside [0, num_pages) reads the last page
+    // and is counted)
+    bool bad = false;
     auto row_off = [&](int r) -> size_t {
-        const int pg = min((unsigned)table[r >> log2_page], (unsigned)(num_pages - 1));
+        const int id = table[r >> log2_page];
+        bad |= (unsigned)id >= (unsigned)num_pages;
+        const int pg = min((unsigned)id, (unsigned)(num_pages - 1));
         return ((size_t)pg * H + hh) * page + (r & (page - 1));
     };
 
@@ -875,6 +890,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_paged_kernel(
         }
         decode_math<D, NS, true>(kv, vv, sk, sv, row0, j1, q, qscale, m, l, acc);
     }
+    if (__ballot(bad) != 0 && lane == 0)
+        __hip_atomic_fetch_add(&g_paged_bad_ids, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     finish_unit<D, FINAL>(m, l, acc, grp, sub, unit, part_ml, part_acc, out);
 }
 
@@ -1205,6 +1222,18 @@ extern "C" int int8k_decode_attention_paged_num_splits(int B, int H, int max_con
     const long long BH = (long long)B * H;
     if (BH >= (1LL << 31)) return 0;
     return plan_paged((int)BH, max_context, head_dim, nsplit).nsplit;
+}
+
+extern "C" int int8k_decode_paged_bad_page_ids(unsigned int* count) {
+    clear_last_error();
+    if (!count) return INT8K_ERR_INVALID_ARGUMENT;
+    const hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_paged_bad_ids),
+                                             sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        set_last_error("hipMemcpyFromSymbol(g_paged_bad_ids)", e);
+        return INT8K_ERR_HIP;
+    }
+    return INT8K_OK;
 }
 
 static int paged_impl(

@@ -63,6 +63,7 @@ _SIGNATURES = {
     "int8k_decode_attention_forward_paged_quant": (_I, [_P] * 10 + [_I] * 8 + [_P, _SZ, _P]),
     "int8k_decode_attention_forward_noalloc": (_I, [_P] * 7 + [_I] * 4 + [_P]),
     "int8k_mlp_sync_timeouts": (_I, [ctypes.POINTER(ctypes.c_uint)]),
+    "int8k_decode_paged_bad_page_ids": (_I, [ctypes.POINTER(ctypes.c_uint)]),
 }
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
@@ -417,6 +418,16 @@ def decode_paged_workspace_bytes(B, H, max_context, D, nsplit=0):
 
 def decode_paged_num_splits(B, H, max_context, D, nsplit=0):
     return load().int8k_decode_attention_paged_num_splits(B, H, max_context, D, nsplit)
+
+
+def decode_paged_bad_page_ids() -> int:
+    """Work units of paged decode calls that met a page id outside [0, num_pages) among the
+    table entries they use, on the current device since the library was loaded;
+    synchronises with the device."""
+    n = ctypes.c_uint(0)
+    check("int8k_decode_paged_bad_page_ids",
+          load().int8k_decode_paged_bad_page_ids(ctypes.byref(n)))
+    return int(n.value)
 
 
 def decode_attention_paged(Qi, K_pages, V_pages, sQ, sK_pages, sV_pages, block_tables,

@@ -5,7 +5,7 @@ tolerances, against the contiguous decode kernel on the same data, and for the
 documented edge behaviour: ragged lengths (1, page-1, page+1, non-multiples of the
 64-row wave iteration), forced split counts, a zero-length sequence and out-of-range
 page ids (any id outside [0, num_pages) reads the last page instead of memory outside
-the cache).
+the cache, and is counted where the sequence uses it).
 """
 import numpy as np
 import pytest
@@ -134,6 +134,29 @@ def test_paged_decode_zero_length_and_clamped_pages(gpu):
     bt_ref = torch.where((bt < 0) | (bt >= NP), torch.full_like(bt, NP - 1), bt)
     ref = _oracle(dict(c, block_tables=bt_ref))
     assert_attn_close(o[1:], ref[1:])
+
+
+@pytest.mark.parametrize("nsplit", [4, 64])
+def test_paged_bad_page_ids_are_counted(gpu, nsplit):
+    # an out-of-range id among the entries a sequence uses is counted (the one-launch kernel
+    # at 4 chunks, the split kernel at 64); ids in entries past a sequence's length are never
+    # read and never counted
+    lens = [1000, 40]
+    c = workloads.paged_case(2, 2, 64, 16, lens, seed=6, device=gpu)
+    NP = c["K_pages"].shape[0]
+    args = lambda bt: (c["Qi"], c["K_pages"], c["V_pages"], c["sQ"], c["sK_pages"],  # noqa: E731
+                       c["sV_pages"], bt, c["context_lens"], c["max_context"])
+    bt = c["block_tables"].clone()
+    bt[1, 3:] = -1             # sequence 1 uses entries 0..2 (40 positions): padding past them
+    assert (capi.decode_paged_num_splits(2, 2, c["max_context"], 64, nsplit) > 8) == (nsplit > 8)
+    before = capi.decode_paged_bad_page_ids()
+    capi.decode_attention_paged(*args(bt), nsplit=nsplit)
+    torch.cuda.synchronize()
+    assert capi.decode_paged_bad_page_ids() == before
+    bt[0, 7] = NP + 1          # positions 112..127 of sequence 0
+    capi.decode_attention_paged(*args(bt), nsplit=nsplit)
+    torch.cuda.synchronize()
+    assert capi.decode_paged_bad_page_ids() >= before + 2   # both heads of sequence 0
 
 
 def test_paged_argument_validation(gpu):
