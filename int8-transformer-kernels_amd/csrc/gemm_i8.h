@@ -214,6 +214,51 @@ __device__ __forceinline__ void sched_reads_mfma() {
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 16 - NR, 0);
 }
 
+// Main-loop operand loads through buffer resources: one 32-bit offset per
+// thread and operand, the chunk index and the K-step adding uniform (scalar)
+// offsets, so a load needs no per-chunk address arithmetic.  The resource
+// covers exactly the operand's bytes ((rows - 1) * ld + cols): rows past the
+// matrix read as zero, and chunks past K (N for a [K][N] B) inside a row are
+// zeroed when stored (EDGE), as with the clamped loads above.
+struct OperandSrc {
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voff;        // this thread's chunk 0 at K-step 0
+    uint32_t chunk_step;  // bytes between chunks i and i+1 of a thread
+    uint32_t k_mul;       // bytes per unit of k0 (1 for K-contiguous, ld for [K][N])
+};
+
+// [rows][ld] K-contiguous operand, tile rows r0 ..: thread t's chunk i is row
+// t/8 + 32 i, bytes (t%8)*16 of the K-step.
+__device__ __forceinline__ OperandSrc operand_rowmajor(const int8_t* P, int rows, int cols, int ld,
+                                                       int r0) {
+    OperandSrc s;
+    s.r = make_buffer(P, (uint32_t)((size_t)(rows - 1) * ld + cols));
+    const int t = threadIdx.x;
+    s.voff = (uint32_t)(r0 + t / kChunksPerRow) * (uint32_t)ld + (t % kChunksPerRow) * 16;
+    s.chunk_step = (uint32_t)(kThreads / kChunksPerRow) * (uint32_t)ld;
+    s.k_mul = 1;
+    return s;
+}
+
+// [K][ldw] N-contiguous B, tile columns n0 ..: thread t's chunk i is k row
+// t/16 + 16 i, bytes (t%16)*16 of the tile's 256 columns.
+__device__ __forceinline__ OperandSrc operand_kn(const int8_t* W, int K, int N, int ldw, int n0) {
+    OperandSrc s;
+    s.r = make_buffer(W, (uint32_t)((size_t)(K - 1) * ldw + N));
+    const int t = threadIdx.x;
+    s.voff = (uint32_t)(t >> 4) * (uint32_t)ldw + (uint32_t)n0 + (t & 15) * 16;
+    s.chunk_step = (uint32_t)(kThreads / 16) * (uint32_t)ldw;
+    s.k_mul = (uint32_t)ldw;
+    return s;
+}
+
+__device__ __forceinline__ int4 load_operand(const OperandSrc& s, int k0, int i) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u w = __builtin_amdgcn_raw_buffer_load_b128(
+        s.r, s.voff, (uint32_t)k0 * s.k_mul + (uint32_t)i * s.chunk_step, 0);
+    return make_int4((int)w.x, (int)w.y, (int)w.z, (int)w.w);
+}
+
 // The MFMA main loop: acc[i][j] (32x32 tiles) of this wave's 128x128 sub-tile.
 //
 // With one wave per SIMD the wave stalls on every MFMA issue, so all other
@@ -251,9 +296,10 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
     const int a_off = (wm * WM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
     const int b_off = BKN ? kn_frag_offset(lane, wn)
                           : A_STAGE + (wn * WN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 16;
-    auto load_b = [&](int k0, int i) {
-        return BKN ? load_chunk_kn(Bt, K, N, ldb, k0, n0, i) : load_chunk(Bt, N, K, ldb, n0, k0, i);
-    };
+    const OperandSrc srcA = operand_rowmajor(A, M, K, lda, m0);
+    const OperandSrc srcB = BKN ? operand_kn(Bt, K, N, ldb, n0) : operand_rowmajor(Bt, N, K, ldb, n0);
+    auto load_a = [&](int k0, int i) { return load_operand(srcA, k0, i); };
+    auto load_b = [&](int k0, int i) { return load_operand(srcB, k0, i); };
     auto store_b = [&](int4 v, char* stage, int k0, int i) {
         if constexpr (BKN) store_chunk_kn<EDGE>(v, stage + A_STAGE, K, N, k0, n0, i);
         else store_chunk<EDGE>(v, stage + A_STAGE, N, K, n0, k0, i);
@@ -272,7 +318,7 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
     Frag f;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
-        f.a[i] = load_chunk(A, M, K, lda, m0, 0, i);
+        f.a[i] = load_a(0, i);
         f.b[i] = load_b(0, i);
     }
 #pragma unroll
@@ -282,7 +328,7 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
     }
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
-        f.a[i] = load_chunk(A, M, K, lda, m0, BK, i);
+        f.a[i] = load_a(BK, i);
         f.b[i] = load_b(BK, i);
     }
     __syncthreads();
@@ -309,7 +355,7 @@ __device__ __forceinline__ void mainloop(v16i (&acc)[TM][TN], const int8_t* __re
             else if (g < 8) b[1][g - 4] = read_b(cur, g - 4, 3);
             if (g < 8) {
                 store_chunk<EDGE>(f.a[g], nxt, M, K, m0, (kt + 1) * BK, g);
-                f.a[g] = load_chunk(A, M, K, lda, m0, (kt + 2) * BK, g);
+                f.a[g] = load_a((kt + 2) * BK, g);
             } else {
                 store_b(f.b[g - 8], nxt, (kt + 1) * BK, g - 8);
                 f.b[g - 8] = load_b((kt + 2) * BK, g - 8);

@@ -1281,9 +1281,20 @@ __global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restr
     }
 }
 
+// The 256 x 256 kernels address each operand through a buffer resource with
+// 32-bit offsets: operands of 4 GiB or more are not taken.
+inline int check_tiled_operands(int M, int N, int K) {
+    if ((size_t)M * K >= (1ull << 32) || (size_t)N * K >= (1ull << 32)) {
+        set_last_error_text("int8 GEMM operand of 4 GiB or more");
+        return INT8K_ERR_UNSUPPORTED;
+    }
+    return INT8K_OK;
+}
+
 template <int EPI, bool BKN = false>
 int launch_gemm(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
                 hipStream_t stream) {
+    if (int st = check_tiled_operands(M, N, K)) return st;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     gemm_i8_kernel<EPI, BKN>
         <<<tiles_m * tiles_n, kThreads, EPI == EPI_I32 ? LDS_BYTES : kEpiLdsBytes, stream>>>(
@@ -1334,6 +1345,7 @@ template <int EPI, bool BKN = false>
 int launch_gemm_rq(const int8_t* A, const int8_t* Bt, int M, int N, int K, const EpiParams& p,
                    int8_t* q, float* scales, uint32_t* amax, uint32_t* arrived,
                    hipStream_t stream) {
+    if (int st = check_tiled_operands(M, N, K)) return st;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     RqParams rq = rq_layout(tiles_m, tiles_n);
     rq.q = q;
