@@ -10,7 +10,8 @@ outputs and scales.  Sampled rows are also checked against the CPU oracle
 (rows are independent under per-token scales).  Shapes: BASELINE config 4,
 ragged rows, columns and K on both GEMMs, a GEMM1-only fusion (GEMM2 on the
 128 x 128 kernel), bias with the per-tensor output, hidden rows beyond the
-fp16 range, and 128 column tiles per stripe (the widest stripe fused).
+fp16 range, 128 column tiles per stripe (the widest stripe fused), and tall
+inputs (16384 and 32768 tokens) whose GEMMs walk 4-8 groups of stripes.
 After each case no tile's wait for its stripe may have given up.
 """
 import numpy as np
@@ -45,6 +46,8 @@ def _check_rows_vs_oracle(c, out, osc, rows, T, dm, bias=None):
     (4000, 4000, 16000),   # ragged rows, columns and K (4000 % 128 = 32) on both GEMMs
     (2048, 2048, 8192),    # GEMM1 fused, GEMM2 on the 128 x 128 kernel
     (768, 2048, 32768),    # 128 column tiles per stripe in GEMM1
+    (16384, 1024, 4096),   # the block benchmark's longest prefill: GEMM1 in 4 dispatch rounds
+    (32768, 1024, 2048),   # 128 stripes of 8 (GEMM1) and 4 (GEMM2) column tiles
 ])
 def test_fused_requant_matches_separate_pass(gpu, T, dm, dff):
     print(f"fused requant T{T} dm{dm} dff{dff}", flush=True)
