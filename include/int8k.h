@@ -260,7 +260,8 @@ int int8k_attention_forward_quant(
 /* being read back from a library global.                                    */
 /* d_model and d_ff must be multiples of 16; T is arbitrary.  x, W1, W2 must */
 /* be 16-byte aligned.  A GEMM operand (x, W1, W2 or the T x d_ff hidden) of */
-/* 4 GiB or more on the large-grid kernels returns INT8K_ERR_UNSUPPORTED.   */
+/* 4 GiB or more on the large-grid kernels returns INT8K_ERR_UNSUPPORTED     */
+/* from the argument checks, before anything is launched.                   */
 /* ------------------------------------------------------------------------ */
 #define INT8K_MLP_WEIGHTS_PREPACKED 1
 #define INT8K_MLP_OUT_PER_TENSOR 2
@@ -299,7 +300,7 @@ int int8k_transpose_int8_weights(const int8_t* W1, const int8_t* W2, int8_t* W1T
 /* Raw C[M,N] = A[M,K] . Bt[N,K]^T with exact int32 accumulation (the MLP's */
 /* GEMM core, kernels/int8_mlp.cu:242-310, exposed so its accumulators can   */
 /* be checked bit-exactly).  K % 16 == 0; A, Bt 16-byte aligned; M*K and    */
-/* N*K below 4 GiB where the 256 x 256 kernel runs (INT8K_ERR_UNSUPPORTED).  */
+/* N*K below 4 GiB (else INT8K_ERR_UNSUPPORTED, before any launch).         */
 int int8k_gemm_i8_i32(const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K,
                       void* stream);
 

@@ -1523,6 +1523,7 @@ extern "C" int int8k_gemm_i8_i32(const int8_t* A, const int8_t* Bt, int32_t* C, 
     if (!A || !Bt || !C || M <= 0 || N <= 0 || K <= 0) return INT8K_ERR_INVALID_ARGUMENT;
     if (K % 16 != 0) return INT8K_ERR_UNSUPPORTED;
     if (!aligned_to(A, 16) || !aligned_to(Bt, 16) || !aligned_to(C, 4)) return INT8K_ERR_MISALIGNED;
+    if (int st = check_tiled_operands(M, N, K)) return st;
     int st = configure_lds();
     if (st != INT8K_OK) return st;
     EpiParams p{};
@@ -1584,6 +1585,11 @@ extern "C" int int8k_mlp_forward(const int8_t* x, const int8_t* W1, const int8_t
     const bool per_tensor_out = (flags & INT8K_MLP_OUT_PER_TENSOR) != 0;
     const MlpPlan pl = mlp_plan(T, d_model, d_ff, flags);
     const RqPlan& rp = pl.rq;
+    // operands of 4 GiB or more on a 256 x 256 GEMM: refused before anything is launched
+    if (tiled_256(T, d_ff, d_model))
+        if (int st = check_tiled_operands(T, d_ff, d_model)) return st;
+    if (tiled_256(T, d_model, d_ff) && !pl.a16)
+        if (int st = check_tiled_operands(T, d_model, d_ff)) return st;
     const MlpWorkspace w = carve_mlp(workspace, T, d_model, d_ff, prepacked, pl);
     if (!workspace || workspace_bytes < w.bytes) return INT8K_ERR_WORKSPACE;
     if (!aligned_to(workspace, 256)) return INT8K_ERR_MISALIGNED;

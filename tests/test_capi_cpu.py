@@ -139,6 +139,25 @@ def test_mlp_argument_validation(capi):
                                  None) == capi.INT8K_ERR_UNSUPPORTED
 
 
+def test_operands_of_4gib_are_refused_before_launch(capi):
+    # the 256 x 256 GEMMs address each operand with 32-bit buffer offsets: a call with an
+    # operand of 4 GiB or more (here the T x d_ff hidden that GEMM2 reads) returns
+    # UNSUPPORTED from its argument checks, with no GPU work enqueued (none exists here)
+    lib = capi.load()
+    T, dm, dff = 1 << 18, 4096, 16384
+    flags = capi.MLP_WEIGHTS_PREPACKED
+    ws_bytes = capi.mlp_workspace_bytes(T, dm, dff, flags)
+    assert ws_bytes > T * dff
+    st = lib.int8k_mlp_forward(_fake(0x10000), _fake(0x20000), _fake(0x30000), _fake(0x40000),
+                               _fake(0x50000), 1, _fake(0x60000), 1, _fake(0x70000), 1, None,
+                               _fake(0x80000), T, dm, dff, flags, _fake(0x100000), ws_bytes,
+                               None)
+    assert st == capi.INT8K_ERR_UNSUPPORTED
+    assert b"4 GiB" in lib.int8k_last_error()
+    assert lib.int8k_gemm_i8_i32(_fake(0x10000), _fake(0x20000), _fake(0x30000), 1 << 16, 256,
+                                 1 << 16, None) == capi.INT8K_ERR_UNSUPPORTED
+
+
 def test_quant_argument_validation(capi):
     lib = capi.load()
     # per-token dequant: unknown dtype, misaligned scales
