@@ -26,7 +26,7 @@ def _oracle(c):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("page", [16, 64, 256])
+@pytest.mark.parametrize("page", [16, 32, 64, 256, 1024])
 def test_paged_decode_matches_oracle(gpu, D, page):
     lens = [1, page - 1, page + 1, 200, 777, 1024]
     c = workloads.paged_case(len(lens), 4, D, page, lens, seed=page + D, device=gpu)
