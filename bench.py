@@ -16,7 +16,8 @@ The default run (`--workload all`) measures every BASELINE configuration:
     4096->16384->4096), config 5 (causal prefill B4 H32 S4096 D128) and the
     end-to-end pre-LN block, INT8 against FP16 (block.py).
 Every figure is the median of 5 windows of `--steps` steps after `--warmup`
-untimed steps, timed with HIP events on the launch stream; every config has
+untimed steps (config 1 and the sweep points: enough steps for ~2 ms windows,
+`steps_per_window`), timed with HIP events on the launch stream; every config has
 its own `roofline` and an oracle parity check (all rows for decode).  Decode
 steps shorter than 50 us also report `graph_us`: the same steps captured in a
 HIP graph and replayed, the device time per step without the host's per-call
@@ -31,6 +32,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -254,7 +256,8 @@ def decode_kernel_label(nsplit):
     return "decode_split_kernel + decode_combine_kernel (one step)"
 
 
-def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False):
+def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False,
+                   min_window_ms=0.0):
     """One decode configuration: seeded inputs, `--warmup` untimed steps, then the median of
     5 windows of `--steps` steps.  Cases whose K+V (+ scales) are under
     512 MB cycle through enough copies of the cache (at least 3, 768 MB in total) that the
@@ -303,8 +306,13 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
                 capi.check("int8k_decode_attention_forward", rc)
         return step
 
+    # a window of a few microsecond-steps is at the mercy of host jitter: the short configs
+    # (min_window_ms > 0) take enough steps per window to last about that long, estimated
+    # from their bytes at 5 TB/s plus ~6 us per launch
+    est_ms = total / 5e12 * 1e3 + 0.006
+    steps = max(args.steps, math.ceil(min_window_ms / est_ms))
     # every cache copy is touched before the first timed window
-    ms, windows = time_windows(step_on(st), args.steps, max(args.warmup, 2 * n_copies), stream)
+    ms, windows = time_windows(step_on(st), steps, max(args.warmup, 2 * n_copies), stream)
     # a short step can be set by the host's issue rate (one ctypes call and one launch per
     # step): its device time is also taken from a captured graph of steps over the copies
     graph_ms = (time_graph(step_on, n_copies * max(1, 40 // n_copies), stream)
@@ -327,7 +335,7 @@ def measure_decode(B, H, D, S, outlier_frac, args, dev, stream, keep_host=False)
            "nsplit": capi.decode_num_splits(BH, S, D, args.nsplit),
            "us": round(ms * 1e3, 2), "TBps": round(tbs, 4),
            "pct_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS * 100, 2),
-           "windows_ms": windows, "cache_copies": n_copies,
+           "windows_ms": windows, "steps_per_window": steps, "cache_copies": n_copies,
            "parity": {"rows_checked": BH, "max_abs": err, "cos": round(cos, 7)}}
     if graph_ms is not None:
         row["graph_us"] = round(graph_ms * 1e3, 2)
@@ -454,7 +462,7 @@ def sweep_rows(args, dev, stream):
     for B, H, D, S, outl in [(1, 12, 64, 1024, 0.0)] + [(8, 32, 64, S, 0.01) for S in (
             2048, 4096, 8192, 16384, 32768)]:
         row, host, _ = measure_decode(B, H, D, S, outl, args, dev, stream,
-                                      keep_host=(B, H, S) == (1, 12, 1024))
+                                      keep_host=(B, H, S) == (1, 12, 1024), min_window_ms=2.0)
         if host is not None:
             cfg1_host = host
         row["roofline"] = hbm_roofline(2 * B * H * S * D, row["us"] / 1e3,
